@@ -1,0 +1,252 @@
+/*
+ * orthocache_hip.h - C ABI of liborthocache_hip.so, the MI355X (gfx950)
+ * implementation of OrthoCache's block-eviction attention path:
+ *   FWHT-512 -> band energies / zeta / block mean / query-aware bound
+ *   -> two-gate mask -> stream compaction -> indirect block-sparse attention.
+ *
+ * Conventions
+ *  - Every pointer argument named as data is a DEVICE pointer (HIP global
+ *    memory), except the argument structs themselves, which live on the host.
+ *  - Layouts follow the reference: keys/values (seq, kv_heads, head_dim),
+ *    queries (seq_q, q_heads, head_dim), head_dim contiguous.  Strides are in
+ *    elements.  Query head hq reads kv head hq / group (GQA; group 1 is the
+ *    reference's equal-heads case).
+ *  - A "segment" is one sequence of a ragged batch (or one layer of a
+ *    multi-layer sweep): cu_blocks[s]..cu_blocks[s+1] are its blocks in the
+ *    flattened block space, whose token range is [cu*512, ...).  cu_blocks ==
+ *    NULL means one segment of total_blocks blocks.
+ *  - Calls are asynchronous on `stream` (a hipStream_t; NULL = default
+ *    stream), never synchronise the host, and never allocate: outputs and
+ *    workspaces are caller-owned.  Counts such as num_active stay on device.
+ *  - Return 0 on success or a negative OC_ERR_* code; oc_last_error() gives
+ *    a message (thread-local).  Entry points are stateless and reentrant.
+ */
+#ifndef ORTHOCACHE_HIP_H
+#define ORTHOCACHE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OC_ABI_VERSION 1
+
+#define OC_OK 0
+#define OC_ERR_INVALID_ARGUMENT (-1)
+#define OC_ERR_UNSUPPORTED (-2)
+#define OC_ERR_HIP (-3)
+#define OC_ERR_WORKSPACE (-4)
+
+/* Element types. */
+#define OC_F32 0
+#define OC_BF16 1
+#define OC_F16 2
+
+#define OC_BLOCK 512 /* FWHT length: tokens per scored block */
+
+/* Thread-local message for the last failing call on this thread. */
+const char* oc_last_error(void);
+int oc_abi_version(void);
+
+/* ---------------------------------------------------------------- FWHT
+ * Replaces fwht_512 (src/orthocache/fwht.py:4-65) and, with n_batch = nb and
+ * strides of (seq, heads*dim), _run_fwht_on_blocks
+ * (src/orthocache/spectral_energy.py:38-66).  y[b, :, c] = H_512 x[b, :, c]
+ * / sqrt(512) in natural (Hadamard) order, fp32 arithmetic.  512 rows per
+ * batch entry, n_cols contiguous columns. */
+typedef struct oc_fwht_args {
+  const void* x;
+  int32_t x_dtype;
+  int64_t x_batch_stride, x_row_stride;
+  void* y;
+  int32_t y_dtype;
+  int64_t y_batch_stride, y_row_stride;
+  int64_t n_cols;
+  int64_t n_batch;
+} oc_fwht_args;
+int oc_fwht512(const oc_fwht_args* a, void* stream);
+
+/* Energy of a coefficient band over a materialised fp32 spectrum
+ * (nb, 512, heads, dim): out[b, h] = sum_{s in [s0, s1)} sum_d spec^2.
+ * Replaces the band sums of compute_spectral_bands for non-default bands
+ * (src/orthocache/spectral_energy.py:100-104). */
+int oc_band_energy(const float* spec, int32_t num_blocks, int32_t num_heads, int32_t head_dim,
+                   int32_t s0, int32_t s1, float* out, void* stream);
+
+/* Spatial block energy sum k^2 per (block, head), any block size.
+ * Replaces compute_block_energy_jax (src/orthocache/spectral_energy.py:21-35). */
+int oc_block_energy(const void* keys, int32_t keys_dtype, int64_t tok_stride, int64_t head_stride,
+                    int32_t head_dim, int32_t num_kv_heads, int32_t num_blocks, int32_t block_size,
+                    float* out, void* stream);
+
+/* ---------------------------------------------------------------- scores
+ * One pass over the keys per (block, kv head): band energies (natural-index
+ * bands DC, [1,64), [64,256), [256,512)), zeta = E_high / (E_low + 1e-6),
+ * DC coefficient, E_AC, and - when q is given - the NaN-propagating max over
+ * the segment's queries (sq tokens x group heads) of the query-aware bound
+ * tau_j = q.kbar/sqrt(d) + ||q|| sqrt(E_AC)/sqrt(d).
+ * Replaces compute_spectral_bands, compute_spectral_decay_ratio,
+ * compute_query_aware_bounds + the max of compute_query_aware_mask
+ * (src/orthocache/spectral_energy.py:69-196).  Block size is 512.
+ * Every output pointer may be NULL.  Requirements: head_dim * esize a multiple
+ * of 16 and head_dim / (16 / esize) in {8,16,32,64,128}; 16-byte aligned keys,
+ * strides multiples of 16 bytes. */
+typedef struct oc_score_args {
+  const void* keys;
+  int32_t keys_dtype;
+  int64_t keys_tok_stride, keys_head_stride;
+  int32_t head_dim, num_kv_heads, total_blocks;
+  const int32_t* cu_blocks; /* device, num_segments + 1, or NULL */
+  int32_t num_segments;
+  const void* q; /* NULL: no bound */
+  int32_t q_dtype;
+  int64_t q_seg_stride, q_tok_stride, q_head_stride;
+  int32_t sq, group;
+  float* tau_max; /* (total_blocks, Hkv) */
+  float* zeta;    /* (total_blocks, Hkv) */
+  float* dc;      /* (total_blocks, Hkv, head_dim) */
+  float* e_low;
+  float* e_mid;
+  float* e_high;
+  float* e_ac;
+} oc_score_args;
+int oc_score_blocks(const oc_score_args* a, void* stream);
+
+/* Query-aware bound for many queries of one segment (prefill), from the dc
+ * and e_ac outputs of oc_score_blocks.  bounds: (sq*group, nb, Hkv) with query
+ * row t*group + g (the GQA-folded layout); tau_part: (ceil(sq*group/32), nb,
+ * Hkv) partial maxima for oc_mask_compact (tau_parts = that count).
+ * Replaces compute_query_aware_bounds (src/orthocache/spectral_energy.py:141-177). */
+typedef struct oc_bound_args {
+  const float* dc;
+  const float* e_ac;
+  const void* q;
+  int32_t q_dtype;
+  int64_t q_tok_stride, q_head_stride;
+  int32_t sq, group, head_dim, num_kv_heads, num_blocks;
+  float* bounds;
+  float* tau_part;
+} oc_bound_args;
+int oc_query_bounds(const oc_bound_args* a, void* stream);
+int32_t oc_query_bound_tiles(int32_t sq, int32_t group);
+
+/* ---------------------------------------------------------------- mask + compaction
+ * keep[j,h] = (max_p tau_max[p,j,h] >= tau) & (zeta[j,h] <= zeta_max), NaN ->
+ * false, thresholds compared in fp32 (compute_multiband_mask,
+ * src/orthocache/spectral_energy.py:199-234), or keep = mask_in when given.
+ * active[j] = OR_h keep[j,h]; indices = per segment the active-first stable
+ * permutation of local block ids, num_active = popcount (stream_compact,
+ * src/orthocache/compaction.py:65-82; src/orthocache/adaptive_attention.py:29-40).
+ * head_indices / head_num_active: the same partition per kv head; with
+ * empty_head_all, a head keeping nothing lists every block and gets
+ * head_uniform = 1 (the all-masked softmax of jax_block_sparse_attention,
+ * src/orthocache/sparse_attention.py:49-57). */
+typedef struct oc_compact_args {
+  const float* tau_max;
+  int32_t tau_parts;
+  const float* zeta;       /* NULL: gate 2 off */
+  const uint8_t* mask_in;  /* (total_blocks, mask_in_heads), instead of scores */
+  int32_t mask_in_heads;
+  const float* tau_arr;    /* device, per segment, or NULL -> tau */
+  float tau;
+  const float* zeta_max_arr;
+  float zeta_max;
+  const int32_t* cu_blocks;
+  int32_t num_segments;
+  int32_t num_kv_heads, total_blocks;
+  uint8_t* mask_out;       /* (total_blocks, Hkv) */
+  uint8_t* active_out;     /* (total_blocks) */
+  int32_t* indices;        /* (total_blocks) */
+  int32_t* num_active;     /* (num_segments) */
+  int32_t* head_indices;   /* (Hkv, total_blocks) */
+  int32_t* head_num_active;/* (num_segments, Hkv) */
+  uint8_t* head_uniform;   /* (num_segments, Hkv) */
+  int32_t empty_head_all;
+} oc_compact_args;
+int oc_mask_compact(const oc_compact_args* a, void* stream);
+
+/* Materialised compaction / decompaction of whole blocks
+ * (stream_compact's gather, src/orthocache/compaction.py:86-98;
+ * stream_decompact, :103-154).  scatter = 0: dst[i] = src[indices[i]] for
+ * i < *num_active, zero otherwise; scatter = 1: dst[indices[i]] = src[i] for
+ * i < *num_active, zero otherwise.  block_bytes must be a multiple of 16. */
+int oc_copy_blocks(const void* src, void* dst, const int32_t* indices, const int32_t* num_active,
+                   int32_t num_blocks, int64_t block_bytes, int32_t scatter, void* stream);
+
+/* ---------------------------------------------------------------- attention
+ * Softmax attention over the tokens of the retained blocks listed by
+ * oc_mask_compact (unified lists, or per-head lists with per_head = 1), fp32
+ * accumulation, output cast to out_dtype; an empty list gives zeros, a
+ * uniform-flagged list gives equal weights over its blocks.
+ * Replaces orthocache_attention / _multihead_loop
+ * (src/orthocache/adaptive_attention.py:46-184), indirect_attention
+ * (src/orthocache/indirect_attention.py:127-170) and the kernel of
+ * compile_pallas_sparse_attention (src/orthocache/sparse_attention.py:67-180).
+ * Decode form: any sq*group (work is split in groups of 8 queries; large
+ * query counts re-read K/V once per group).  head_dim/(16/esize) in
+ * {8,16,32,64}.  workspace >= oc_attend_workspace_size(...). */
+typedef struct oc_attend_args {
+  const void* q;
+  int32_t q_dtype;
+  int64_t q_seg_stride, q_tok_stride, q_head_stride;
+  const void* k;
+  const void* v;
+  int32_t kv_dtype;
+  int64_t k_tok_stride, k_head_stride, v_tok_stride, v_head_stride;
+  int32_t head_dim, num_kv_heads, group, sq;
+  int32_t block_size, total_blocks;
+  const int32_t* cu_blocks;
+  int32_t num_segments;
+  const int32_t* indices;
+  const int32_t* counts;
+  int32_t per_head;
+  const uint8_t* uniform;
+  void* out;
+  int32_t out_dtype;
+  int64_t out_seg_stride, out_tok_stride, out_head_stride;
+} oc_attend_args;
+size_t oc_attend_workspace_size(const oc_attend_args* a);
+int oc_attend(const oc_attend_args* a, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- one layer
+ * The hot path in one call: oc_score_blocks -> oc_mask_compact -> oc_attend
+ * (what orthocache_forward(mode='compact') does with a given tau and
+ * zeta_max, src/orthocache/pipeline.py:96-145), for a batch of segments with
+ * per-segment thresholds.  Optional outputs (tau_max, zeta, mask, indices,
+ * num_active) may be NULL, in which case the workspace holds them.
+ * workspace >= oc_decode_layer_workspace_size(...). */
+typedef struct oc_layer_args {
+  const void* q;
+  int32_t q_dtype;
+  int64_t q_seg_stride, q_tok_stride, q_head_stride;
+  const void* k;
+  const void* v;
+  int32_t kv_dtype;
+  int64_t k_tok_stride, k_head_stride, v_tok_stride, v_head_stride;
+  int32_t head_dim, num_kv_heads, group, sq;
+  int32_t total_blocks;
+  const int32_t* cu_blocks;
+  int32_t num_segments;
+  const float* tau_arr;
+  float tau;
+  const float* zeta_max_arr;
+  float zeta_max;
+  void* out;
+  int32_t out_dtype;
+  int64_t out_seg_stride, out_tok_stride, out_head_stride;
+  float* tau_max;
+  float* zeta;
+  uint8_t* mask;
+  int32_t* indices;
+  int32_t* num_active;
+} oc_layer_args;
+size_t oc_decode_layer_workspace_size(const oc_layer_args* a);
+int oc_decode_layer(const oc_layer_args* a, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ORTHOCACHE_HIP_H */

@@ -1,0 +1,424 @@
+"""Thin wrappers: torch tensors -> liborthocache_hip.so calls.
+
+Every function launches HIP kernels on the tensors' device, on torch's
+current stream, and returns device tensors.  No host synchronisation
+happens here.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import torch
+
+from . import _native as N
+from ._native import BLOCK, check, dtype_code, lib, ptr, require_gpu, stream_ptr
+
+
+def _kv_view(t: torch.Tensor, name: str) -> torch.Tensor:
+    """(S, H, D) with unit dim stride and 16-byte aligned rows, else a copy."""
+    if t.dim() != 3:
+        raise ValueError(f"{name} must be (seq, heads, head_dim), got shape {tuple(t.shape)}")
+    es = t.element_size()
+    ok = (t.stride(2) == 1 and t.data_ptr() % 16 == 0 and (t.stride(0) * es) % 16 == 0
+          and (t.stride(1) * es) % 16 == 0)
+    return t if ok else t.contiguous()
+
+
+def _q_view(t: torch.Tensor, name: str = "q") -> torch.Tensor:
+    if t.stride(-1) != 1:
+        t = t.contiguous()
+    return t
+
+
+def kv_group(q_heads: int, kv_heads: int) -> int:
+    if q_heads % kv_heads:
+        raise ValueError(f"query heads ({q_heads}) must be a multiple of kv heads ({kv_heads})")
+    return q_heads // kv_heads
+
+
+# ------------------------------------------------------------------- FWHT
+def fwht_rows(x: torch.Tensor, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """FWHT along dim -2 of a (batch, 512, ncols) tensor (columns contiguous)."""
+    require_gpu(x)
+    if x.dim() != 3 or x.shape[1] != BLOCK:
+        raise ValueError("fwht_rows expects (batch, 512, ncols)")
+    if x.stride(2) != 1:
+        x = x.contiguous()
+    y = torch.empty(x.shape, dtype=out_dtype or x.dtype, device=x.device)
+    a = N.FwhtArgs(ptr(x), dtype_code(x.dtype), x.stride(0), x.stride(1),
+                   ptr(y), dtype_code(y.dtype), y.stride(0), y.stride(1), x.shape[2], x.shape[0])
+    check(lib().oc_fwht512(C.byref(a), stream_ptr(x.device)), "oc_fwht512")
+    return y
+
+
+def band_energy(spec: torch.Tensor, s0: int, s1: int) -> torch.Tensor:
+    """sum_{s in [s0,s1)} sum_d spec[b, s, h, d]^2 for a (nb, 512, H, D) fp32 spectrum."""
+    spec = spec.contiguous()
+    nb, _, h, d = spec.shape
+    out = torch.empty((nb, h), dtype=torch.float32, device=spec.device)
+    check(lib().oc_band_energy(ptr(spec), nb, h, d, s0, s1, ptr(out), stream_ptr(spec.device)),
+          "oc_band_energy")
+    return out
+
+
+def block_energy(keys: torch.Tensor, block_size: int) -> torch.Tensor:
+    require_gpu(keys)
+    keys = _kv_view(keys, "keys")
+    s, h, d = keys.shape
+    nb = s // block_size
+    out = torch.empty((nb, h), dtype=torch.float32, device=keys.device)
+    check(lib().oc_block_energy(ptr(keys), dtype_code(keys.dtype), keys.stride(0), keys.stride(1), d, h,
+                                nb, block_size, ptr(out), stream_ptr(keys.device)), "oc_block_energy")
+    return out
+
+
+# ----------------------------------------------------------------- scores
+@dataclass
+class Scores:
+    tau_max: torch.Tensor | None   # (P, nb, Hkv) partial maxima over query tiles
+    zeta: torch.Tensor | None      # (nb, Hkv)
+    dc: torch.Tensor | None = None
+    e_low: torch.Tensor | None = None
+    e_mid: torch.Tensor | None = None
+    e_high: torch.Tensor | None = None
+    e_ac: torch.Tensor | None = None
+    bounds: torch.Tensor | None = None  # (Sq*G, nb, Hkv)
+
+
+INLINE_QUERY_LIMIT = 16
+
+
+def score(keys: torch.Tensor, q: torch.Tensor | None = None, *, want_bands: bool = False,
+          want_bounds: bool = False, want_zeta: bool = True, cu_blocks: torch.Tensor | None = None,
+          num_segments: int = 1) -> Scores:
+    """One pass over the keys: zeta, bands and (with q) the query-aware bound.
+
+    keys: (S, Hkv, D), S a multiple of 512.  q: (Sq, Hq, D) for one segment or
+    (B, Sq, Hq, D) with cu_blocks for several.  Small query counts get their
+    maximum bound inline; large ones (or want_bounds) go through the tiled
+    bound kernel.
+    """
+    require_gpu(keys, q, cu_blocks)
+    keys = _kv_view(keys, "keys")
+    s, hkv, d = keys.shape
+    if s % BLOCK:
+        raise ValueError(f"seq_len {s} is not a multiple of the block size {BLOCK}")
+    nb = s // BLOCK
+    dev = keys.device
+    f32 = dict(dtype=torch.float32, device=dev)
+    tiles = (nb, hkv)
+    zeta = torch.empty(tiles, **f32) if want_zeta else None
+    res = Scores(tau_max=None, zeta=zeta)
+    sq = group = 0
+    q_ok = q is not None
+    if q_ok:
+        q = _q_view(q)
+        if cu_blocks is None:
+            if q.dim() != 3:
+                raise ValueError("q must be (seq_q, heads, head_dim)")
+            sq, hq, qd = q.shape
+            qseg = 0
+        else:
+            if q.dim() != 4:
+                raise ValueError("with cu_blocks, q must be (segments, seq_q, heads, head_dim)")
+            _, sq, hq, qd = q.shape
+            qseg = q.stride(0)
+        if qd != d:
+            raise ValueError(f"q head_dim {qd} != keys head_dim {d}")
+        group = kv_group(hq, hkv)
+    nq = sq * group
+    inline = q_ok and not want_bounds and nq <= INLINE_QUERY_LIMIT
+    need_dc = want_bands or (q_ok and not inline)
+    if want_bands or need_dc:
+        res.dc = torch.empty((nb, hkv, d), **f32)
+        res.e_ac = torch.empty(tiles, **f32)
+    if want_bands:
+        res.e_low = torch.empty(tiles, **f32)
+        res.e_mid = torch.empty(tiles, **f32)
+        res.e_high = torch.empty(tiles, **f32)
+    if inline:
+        res.tau_max = torch.empty((1,) + tiles, **f32)
+    a = N.ScoreArgs()
+    a.keys = ptr(keys); a.keys_dtype = dtype_code(keys.dtype)
+    a.keys_tok_stride = keys.stride(0); a.keys_head_stride = keys.stride(1)
+    a.head_dim = d; a.num_kv_heads = hkv; a.total_blocks = nb
+    a.cu_blocks = ptr(cu_blocks); a.num_segments = num_segments
+    if inline:
+        a.q = ptr(q); a.q_dtype = dtype_code(q.dtype)
+        a.q_seg_stride = q.stride(0) if cu_blocks is not None else 0
+        a.q_tok_stride = q.stride(-3); a.q_head_stride = q.stride(-2)
+        a.sq = sq; a.group = group
+        a.tau_max = ptr(res.tau_max)
+    a.zeta = ptr(res.zeta); a.dc = ptr(res.dc); a.e_low = ptr(res.e_low); a.e_mid = ptr(res.e_mid)
+    a.e_high = ptr(res.e_high); a.e_ac = ptr(res.e_ac)
+    check(lib().oc_score_blocks(C.byref(a), stream_ptr(dev)), "oc_score_blocks")
+    if q_ok and not inline:
+        if cu_blocks is not None:
+            raise ValueError("many-query bounds need a single segment")
+        ntiles = int(lib().oc_query_bound_tiles(sq, group))
+        res.tau_max = torch.empty((ntiles,) + tiles, **f32)
+        if want_bounds:
+            res.bounds = torch.empty((nq, nb, hkv), **f32)
+        b = N.BoundArgs(ptr(res.dc), ptr(res.e_ac), ptr(q), dtype_code(q.dtype), q.stride(0), q.stride(1),
+                        sq, group, d, hkv, nb, ptr(res.bounds), ptr(res.tau_max))
+        check(lib().oc_query_bounds(C.byref(b), stream_ptr(dev)), "oc_query_bounds")
+    return res
+
+
+# ------------------------------------------------------ mask + compaction
+@dataclass
+class Compacted:
+    mask: torch.Tensor | None          # (nb, Hkv) bool
+    active: torch.Tensor | None        # (nb,) bool
+    indices: torch.Tensor | None       # (nb,) int32 permutation
+    num_active: torch.Tensor | None    # (segments,) int32
+    head_indices: torch.Tensor | None = None     # (Hkv, nb) int32
+    head_num_active: torch.Tensor | None = None  # (segments, Hkv) int32
+    head_uniform: torch.Tensor | None = None     # (segments, Hkv) uint8
+
+
+def mask_compact(*, num_blocks: int, num_kv_heads: int, device: torch.device,
+                 tau_max: torch.Tensor | None = None, zeta: torch.Tensor | None = None,
+                 tau=None, zeta_max=None, mask_in: torch.Tensor | None = None,
+                 want_mask: bool = False, want_active: bool = False, want_indices: bool = True,
+                 want_head_lists: bool = False, empty_head_all: bool = False,
+                 cu_blocks: torch.Tensor | None = None, num_segments: int = 1) -> Compacted:
+    """Two-gate mask (or a given mask) -> masks, permutation and counts, on device.
+
+    tau / zeta_max: Python floats (rounded to fp32 as JAX does) or per-segment
+    fp32 device tensors.  A gate whose input is None is off.
+    """
+    nb, hkv = num_blocks, num_kv_heads
+    a = N.CompactArgs()
+    if mask_in is not None:
+        if mask_in.dtype != torch.bool:
+            mask_in = mask_in != 0
+        m = mask_in.contiguous().view(torch.uint8)
+        if m.dim() == 1:
+            heads_in = 1
+        elif m.dim() == 2 and m.shape[1] in (1, hkv):
+            heads_in = m.shape[1]
+        else:
+            raise ValueError(f"block_mask must be (num_blocks,) or (num_blocks, {hkv}), got {tuple(m.shape)}")
+        if m.shape[0] != nb:
+            raise ValueError(f"block_mask has {m.shape[0]} blocks, expected {nb}")
+        a.mask_in = ptr(m); a.mask_in_heads = heads_in
+    else:
+        if tau_max is None:
+            raise ValueError("need scores or a mask")
+        tau_max = tau_max.contiguous()
+        a.tau_max = ptr(tau_max); a.tau_parts = tau_max.shape[0] if tau_max.dim() == 3 else 1
+        if zeta is not None:
+            zeta = zeta.contiguous()
+            a.zeta = ptr(zeta)
+        if isinstance(tau, torch.Tensor):
+            tau = tau.to(device=device, dtype=torch.float32).contiguous()
+            a.tau_arr = ptr(tau)
+        else:
+            a.tau = float(tau)
+        if zeta is not None:
+            if isinstance(zeta_max, torch.Tensor):
+                zeta_max = zeta_max.to(device=device, dtype=torch.float32).contiguous()
+                a.zeta_max_arr = ptr(zeta_max)
+            else:
+                a.zeta_max = float(zeta_max)
+    a.cu_blocks = ptr(cu_blocks); a.num_segments = num_segments
+    a.num_kv_heads = hkv; a.total_blocks = nb
+    u8 = dict(dtype=torch.uint8, device=device)
+    i32 = dict(dtype=torch.int32, device=device)
+    res = Compacted(None, None, None, None)
+    if want_mask:
+        res.mask = torch.empty((nb, hkv), **u8)
+        a.mask_out = ptr(res.mask)
+    if want_active:
+        res.active = torch.empty((nb,), **u8)
+        a.active_out = ptr(res.active)
+    if want_indices:
+        res.indices = torch.empty((nb,), **i32)
+        res.num_active = torch.empty((num_segments,), **i32)
+        a.indices = ptr(res.indices); a.num_active = ptr(res.num_active)
+    if want_head_lists:
+        res.head_indices = torch.empty((hkv, nb), **i32)
+        res.head_num_active = torch.empty((num_segments, hkv), **i32)
+        res.head_uniform = torch.empty((num_segments, hkv), **u8)
+        a.head_indices = ptr(res.head_indices); a.head_num_active = ptr(res.head_num_active)
+        a.head_uniform = ptr(res.head_uniform); a.empty_head_all = 1 if empty_head_all else 0
+    check(lib().oc_mask_compact(C.byref(a), stream_ptr(device)), "oc_mask_compact")
+    if res.mask is not None:
+        res.mask = res.mask.view(torch.bool)
+    if res.active is not None:
+        res.active = res.active.view(torch.bool)
+    return res
+
+
+def copy_blocks(src: torch.Tensor, dst: torch.Tensor, indices: torch.Tensor, num_active: torch.Tensor,
+                num_blocks: int, scatter: bool) -> None:
+    block_bytes = src.numel() * src.element_size() // max(1, src.shape[0])
+    check(lib().oc_copy_blocks(ptr(src), ptr(dst), ptr(indices), ptr(num_active), num_blocks, block_bytes,
+                               1 if scatter else 0, stream_ptr(src.device)), "oc_copy_blocks")
+
+
+# --------------------------------------------------------------- attention
+def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, indices: torch.Tensor, counts: torch.Tensor, *,
+           block_size: int = BLOCK, per_head: bool = False, uniform: torch.Tensor | None = None,
+           out_dtype: torch.dtype | None = None, cu_blocks: torch.Tensor | None = None,
+           num_segments: int = 1, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Attention over the listed blocks.  q: (Sq, Hq, D) (or (B, Sq, Hq, D) with
+    cu_blocks); k, v: (S, Hkv, D).  Returns q-shaped output in out_dtype."""
+    require_gpu(q, k, v, indices, counts)
+    k = _kv_view(k, "keys")
+    v = _kv_view(v, "values")
+    q = _q_view(q)
+    s, hkv, d = k.shape
+    if v.shape != k.shape:
+        raise ValueError(f"values shape {tuple(v.shape)} != keys shape {tuple(k.shape)}")
+    if s % block_size:
+        raise ValueError(f"seq_len {s} is not a multiple of block_size {block_size}")
+    if q.shape[-1] != d:
+        raise ValueError(f"q head_dim {q.shape[-1]} != keys head_dim {d}")
+    group = kv_group(q.shape[-2], hkv)
+    sq = q.shape[-3]
+    if out is None:
+        out = torch.empty(q.shape, dtype=out_dtype or q.dtype, device=q.device)
+    a = N.AttendArgs()
+    a.q = ptr(q); a.q_dtype = dtype_code(q.dtype)
+    a.q_seg_stride = q.stride(0) if q.dim() == 4 else 0
+    a.q_tok_stride = q.stride(-3); a.q_head_stride = q.stride(-2)
+    a.k = ptr(k); a.v = ptr(v); a.kv_dtype = dtype_code(k.dtype)
+    if v.dtype != k.dtype:
+        raise ValueError("keys and values must share a dtype")
+    a.k_tok_stride = k.stride(0); a.k_head_stride = k.stride(1)
+    a.v_tok_stride = v.stride(0); a.v_head_stride = v.stride(1)
+    a.head_dim = d; a.num_kv_heads = hkv; a.group = group; a.sq = sq
+    a.block_size = block_size; a.total_blocks = s // block_size
+    a.cu_blocks = ptr(cu_blocks); a.num_segments = num_segments
+    a.indices = ptr(indices); a.counts = ptr(counts); a.per_head = 1 if per_head else 0
+    a.uniform = ptr(uniform)
+    a.out = ptr(out); a.out_dtype = dtype_code(out.dtype)
+    a.out_seg_stride = out.stride(0) if out.dim() == 4 else 0
+    a.out_tok_stride = out.stride(-3); a.out_head_stride = out.stride(-2)
+    L = lib()
+    ws_bytes = int(L.oc_attend_workspace_size(C.byref(a)))
+    if ws_bytes == 0 and a.total_blocks > 0:
+        # Size query failed validation: surface the message.
+        check(L.oc_attend(C.byref(a), None, 0, stream_ptr(q.device)), "oc_attend")
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=q.device)
+    check(L.oc_attend(C.byref(a), ptr(ws), ws_bytes, stream_ptr(q.device)), "oc_attend")
+    return out
+
+
+# ------------------------------------------------------------- one layer
+class DecodeLayer:
+    """Pre-bound score -> compact -> attend for fixed shapes (reusable workspace).
+
+    keys/values (S, Hkv, D) packed over segments; q (B, Sq, Hq, D) when
+    cu_blocks is given, else (Sq, Hq, D).  Call ``run()`` to launch the three
+    kernels on the current stream.
+    """
+
+    def __init__(self, q, k, v, tau, zeta_max, *, cu_blocks=None, num_segments=1, out=None,
+                 out_dtype=None, keep_scores=True):
+        require_gpu(q, k, v, cu_blocks)
+        self.k = _kv_view(k, "keys")
+        self.v = _kv_view(v, "values")
+        self.q = _q_view(q)
+        s, hkv, d = self.k.shape
+        if s % BLOCK:
+            raise ValueError(f"seq_len {s} is not a multiple of {BLOCK}")
+        nb = s // BLOCK
+        dev = self.k.device
+        self.device = dev
+        group = kv_group(self.q.shape[-2], hkv)
+        self.out = out if out is not None else torch.empty(self.q.shape, dtype=out_dtype or self.q.dtype, device=dev)
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.tau_max = torch.empty((nb, hkv), **f32) if keep_scores else None
+        self.zeta = torch.empty((nb, hkv), **f32) if keep_scores else None
+        self.indices = torch.empty((nb,), dtype=torch.int32, device=dev)
+        self.num_active = torch.empty((num_segments,), dtype=torch.int32, device=dev)
+        a = N.LayerArgs()
+        q_ = self.q
+        a.q = ptr(q_); a.q_dtype = dtype_code(q_.dtype)
+        a.q_seg_stride = q_.stride(0) if q_.dim() == 4 else 0
+        a.q_tok_stride = q_.stride(-3); a.q_head_stride = q_.stride(-2)
+        a.k = ptr(self.k); a.v = ptr(self.v); a.kv_dtype = dtype_code(self.k.dtype)
+        a.k_tok_stride = self.k.stride(0); a.k_head_stride = self.k.stride(1)
+        a.v_tok_stride = self.v.stride(0); a.v_head_stride = self.v.stride(1)
+        a.head_dim = d; a.num_kv_heads = hkv; a.group = group; a.sq = q_.shape[-3]
+        a.total_blocks = nb; a.cu_blocks = ptr(cu_blocks); a.num_segments = num_segments
+        self._tau_t = self._zmax_t = None
+        if isinstance(tau, torch.Tensor):
+            self._tau_t = tau.to(device=dev, dtype=torch.float32).contiguous()
+            a.tau_arr = ptr(self._tau_t)
+        else:
+            a.tau = float(tau)
+        if isinstance(zeta_max, torch.Tensor):
+            self._zmax_t = zeta_max.to(device=dev, dtype=torch.float32).contiguous()
+            a.zeta_max_arr = ptr(self._zmax_t)
+        else:
+            a.zeta_max = float(zeta_max)
+        a.out = ptr(self.out); a.out_dtype = dtype_code(self.out.dtype)
+        o = self.out
+        a.out_seg_stride = o.stride(0) if o.dim() == 4 else 0
+        a.out_tok_stride = o.stride(-3); a.out_head_stride = o.stride(-2)
+        a.tau_max = ptr(self.tau_max); a.zeta = ptr(self.zeta)
+        a.indices = ptr(self.indices); a.num_active = ptr(self.num_active)
+        self.cu_blocks = cu_blocks
+        self.args = a
+        L = lib()
+        ws = int(L.oc_decode_layer_workspace_size(C.byref(a)))
+        if ws == 0:
+            check(L.oc_decode_layer(C.byref(a), None, 0, 0), "oc_decode_layer")
+        self.workspace = torch.empty((ws,), dtype=torch.uint8, device=dev)
+        self._ws_ptr = ptr(self.workspace)
+        self._ws_bytes = ws
+        self._fn = L.oc_decode_layer
+        self._argp = C.byref(a)
+
+    def run(self, stream: int | None = None) -> torch.Tensor:
+        s = stream_ptr(self.device) if stream is None else stream
+        check(self._fn(self._argp, self._ws_ptr, self._ws_bytes, s), "oc_decode_layer")
+        return self.out
+
+    def phases(self):
+        """Callables launching the layer's three phases one at a time on the
+        current stream, with the same arguments as run() (for per-kernel timing)."""
+        a = self.args
+        L = lib()
+        sa = N.ScoreArgs()
+        sa.keys = a.k; sa.keys_dtype = a.kv_dtype; sa.keys_tok_stride = a.k_tok_stride
+        sa.keys_head_stride = a.k_head_stride; sa.head_dim = a.head_dim; sa.num_kv_heads = a.num_kv_heads
+        sa.total_blocks = a.total_blocks; sa.cu_blocks = a.cu_blocks; sa.num_segments = a.num_segments
+        sa.q = a.q; sa.q_dtype = a.q_dtype; sa.q_seg_stride = a.q_seg_stride; sa.q_tok_stride = a.q_tok_stride
+        sa.q_head_stride = a.q_head_stride; sa.sq = a.sq; sa.group = a.group
+        sa.tau_max = a.tau_max; sa.zeta = a.zeta
+        ca = N.CompactArgs()
+        ca.tau_max = a.tau_max; ca.tau_parts = 1; ca.zeta = a.zeta
+        ca.tau_arr = a.tau_arr; ca.tau = a.tau; ca.zeta_max_arr = a.zeta_max_arr; ca.zeta_max = a.zeta_max
+        ca.cu_blocks = a.cu_blocks; ca.num_segments = a.num_segments
+        ca.num_kv_heads = a.num_kv_heads; ca.total_blocks = a.total_blocks
+        ca.indices = a.indices; ca.num_active = a.num_active
+        ta = N.AttendArgs()
+        for f in ("q", "q_dtype", "q_seg_stride", "q_tok_stride", "q_head_stride", "k", "v", "kv_dtype",
+                  "k_tok_stride", "k_head_stride", "v_tok_stride", "v_head_stride", "head_dim", "num_kv_heads",
+                  "group", "sq", "total_blocks", "cu_blocks", "num_segments", "out", "out_dtype",
+                  "out_seg_stride", "out_tok_stride", "out_head_stride"):
+            setattr(ta, f, getattr(a, f))
+        ta.block_size = BLOCK; ta.indices = a.indices; ta.counts = a.num_active
+        ws = int(L.oc_attend_workspace_size(C.byref(ta)))
+        self._phase_ws = torch.empty((max(ws, 1),), dtype=torch.uint8, device=self.device)
+        self._phase_args = (sa, ca, ta)
+        dev = self.device
+        wsp = ptr(self._phase_ws)
+
+        def score():
+            check(L.oc_score_blocks(C.byref(sa), stream_ptr(dev)), "oc_score_blocks")
+
+        def compact():
+            check(L.oc_mask_compact(C.byref(ca), stream_ptr(dev)), "oc_mask_compact")
+
+        def attend():
+            check(L.oc_attend(C.byref(ta), wsp, ws, stream_ptr(dev)), "oc_attend")
+
+        return score, compact, attend

@@ -1,0 +1,320 @@
+// C ABI of liborthocache_hip.so: argument validation, workspace layout and
+// kernel launches.  Declarations and semantics: include/orthocache_hip.h.
+#include "oc_kernels.h"
+#include "../../include/orthocache_hip.h"
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(OC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return OC_OK;
+}
+
+bool valid_dtype(int dt) { return dt == OC_F32 || dt == OC_BF16 || dt == OC_F16; }
+int esize(int dt) { return dt == OC_F32 ? 4 : 2; }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+int check_kv(const char* name, const void* p, int dt, int64_t tok_stride, int64_t head_stride, int head_dim) {
+  if (!p) return fail(OC_ERR_INVALID_ARGUMENT, "%s is NULL", name);
+  if (!valid_dtype(dt)) return fail(OC_ERR_INVALID_ARGUMENT, "%s: unknown dtype %d", name, dt);
+  const int es = esize(dt);
+  if (!aligned16(p) || (tok_stride * es) % 16 || (head_stride * es) % 16 || (head_dim * es) % 16)
+    return fail(OC_ERR_INVALID_ARGUMENT,
+                "%s must be 16-byte aligned with 16-byte multiple strides (tok %lld, head %lld, dim %d)",
+                name, (long long)tok_stride, (long long)head_stride, head_dim);
+  return OC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* oc_last_error(void) { return g_err; }
+int oc_abi_version(void) { return OC_ABI_VERSION; }
+
+int oc_fwht512(const oc_fwht_args* a, void* stream) {
+  if (!a) return fail(OC_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (!a->x || !a->y) return fail(OC_ERR_INVALID_ARGUMENT, "x or y is NULL");
+  if (!valid_dtype(a->x_dtype) || !valid_dtype(a->y_dtype))
+    return fail(OC_ERR_INVALID_ARGUMENT, "unknown dtype");
+  if (a->n_cols < 0 || a->n_batch < 0) return fail(OC_ERR_INVALID_ARGUMENT, "negative size");
+  if ((a->n_cols + 31) / 32 * a->n_batch > 0x7fffffffLL) return fail(OC_ERR_UNSUPPORTED, "too many tiles");
+  oc::FwhtParams p{a->x, a->x_dtype, a->x_batch_stride, a->x_row_stride, a->y, a->y_dtype,
+                   a->y_batch_stride, a->y_row_stride, a->n_cols, a->n_batch};
+  return hip_check(oc::launch_fwht(p, (hipStream_t)stream), "oc_fwht512");
+}
+
+int oc_band_energy(const float* spec, int32_t num_blocks, int32_t num_heads, int32_t head_dim,
+                   int32_t s0, int32_t s1, float* out, void* stream) {
+  if (!spec || !out) return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (num_blocks < 0 || num_heads <= 0 || head_dim <= 0 || s0 < 0 || s1 > OC_BLOCK || s0 > s1)
+    return fail(OC_ERR_INVALID_ARGUMENT, "bad band [%d, %d) or shape", s0, s1);
+  oc::BandParams p{spec, num_blocks, num_heads, head_dim, s0, s1, out};
+  return hip_check(oc::launch_band_energy(p, (hipStream_t)stream), "oc_band_energy");
+}
+
+int oc_block_energy(const void* keys, int32_t keys_dtype, int64_t tok_stride, int64_t head_stride,
+                    int32_t head_dim, int32_t num_kv_heads, int32_t num_blocks, int32_t block_size,
+                    float* out, void* stream) {
+  if (!keys || !out) return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (!valid_dtype(keys_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "unknown dtype");
+  if (head_dim <= 0 || num_kv_heads <= 0 || num_blocks < 0 || block_size <= 0)
+    return fail(OC_ERR_INVALID_ARGUMENT, "bad shape");
+  oc::EnergyParams p{keys, keys_dtype, tok_stride, head_stride, head_dim, num_kv_heads, num_blocks,
+                     block_size, out};
+  return hip_check(oc::launch_block_energy(p, (hipStream_t)stream), "oc_block_energy");
+}
+
+int oc_score_blocks(const oc_score_args* a, void* stream) {
+  if (!a) return fail(OC_ERR_INVALID_ARGUMENT, "args is NULL");
+  int rc = check_kv("keys", a->keys, a->keys_dtype, a->keys_tok_stride, a->keys_head_stride, a->head_dim);
+  if (rc) return rc;
+  if (!oc::score_supported(a->keys_dtype, a->head_dim))
+    return fail(OC_ERR_UNSUPPORTED, "head_dim %d unsupported for dtype %d (need head_dim/(16/esize) in {8..128} power of 2)",
+                a->head_dim, a->keys_dtype);
+  if (a->num_kv_heads <= 0 || a->total_blocks < 0) return fail(OC_ERR_INVALID_ARGUMENT, "bad shape");
+  if ((int64_t)a->total_blocks * a->num_kv_heads > 0x7fffffffLL) return fail(OC_ERR_UNSUPPORTED, "too many tiles");
+  if (a->cu_blocks && a->num_segments <= 0) return fail(OC_ERR_INVALID_ARGUMENT, "cu_blocks needs num_segments > 0");
+  if (a->q) {
+    if (!valid_dtype(a->q_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "q: unknown dtype");
+    if (a->sq < 0 || a->group <= 0) return fail(OC_ERR_INVALID_ARGUMENT, "bad sq/group");
+  }
+  oc::ScoreParams p{a->keys, a->keys_tok_stride, a->keys_head_stride, a->keys_dtype, a->head_dim,
+                    a->num_kv_heads, a->total_blocks, a->cu_blocks, a->cu_blocks ? a->num_segments : 1,
+                    a->q, a->q_dtype, a->q_seg_stride, a->q_tok_stride, a->q_head_stride, a->sq, a->group,
+                    a->tau_max, a->zeta, a->dc, a->e_low, a->e_mid, a->e_high, a->e_ac};
+  return hip_check(oc::launch_score(p, (hipStream_t)stream), "oc_score_blocks");
+}
+
+int32_t oc_query_bound_tiles(int32_t sq, int32_t group) { return (sq * group + 31) / 32; }
+
+int oc_query_bounds(const oc_bound_args* a, void* stream) {
+  if (!a) return fail(OC_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (!a->dc || !a->e_ac || !a->q) return fail(OC_ERR_INVALID_ARGUMENT, "NULL input");
+  if (!valid_dtype(a->q_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "q: unknown dtype");
+  if (a->head_dim <= 0 || a->head_dim > 1024 || a->num_kv_heads <= 0 || a->num_blocks < 0 || a->sq < 0 || a->group <= 0)
+    return fail(OC_ERR_INVALID_ARGUMENT, "bad shape");
+  const int64_t grid = (int64_t)oc_query_bound_tiles(a->sq, a->group) * ((a->num_blocks + 7) / 8) * a->num_kv_heads;
+  if (grid > 0x7fffffffLL) return fail(OC_ERR_UNSUPPORTED, "too many tiles");
+  oc::BoundParams p{a->dc, a->e_ac, a->q, a->q_dtype, a->q_tok_stride, a->q_head_stride, a->sq, a->group,
+                    a->head_dim, a->num_kv_heads, a->num_blocks, a->bounds, a->tau_part};
+  return hip_check(oc::launch_bound(p, (hipStream_t)stream), "oc_query_bounds");
+}
+
+int oc_mask_compact(const oc_compact_args* a, void* stream) {
+  if (!a) return fail(OC_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (!a->mask_in && !a->tau_max) return fail(OC_ERR_INVALID_ARGUMENT, "need tau_max or mask_in");
+  if (a->mask_in && a->mask_in_heads != 1 && a->mask_in_heads != a->num_kv_heads)
+    return fail(OC_ERR_INVALID_ARGUMENT, "mask_in_heads must be 1 or num_kv_heads");
+  if (a->num_kv_heads <= 0 || a->total_blocks < 0) return fail(OC_ERR_INVALID_ARGUMENT, "bad shape");
+  if (a->tau_max && a->tau_parts <= 0) return fail(OC_ERR_INVALID_ARGUMENT, "tau_parts must be > 0");
+  if (a->cu_blocks && a->num_segments <= 0) return fail(OC_ERR_INVALID_ARGUMENT, "cu_blocks needs num_segments > 0");
+  if (a->indices && !a->num_active) return fail(OC_ERR_INVALID_ARGUMENT, "indices needs num_active");
+  if (a->head_indices && !a->head_num_active) return fail(OC_ERR_INVALID_ARGUMENT, "head_indices needs head_num_active");
+  oc::CompactParams p{a->tau_max, a->tau_parts, a->zeta, a->mask_in, a->mask_in_heads,
+                      a->tau_arr, a->tau, a->zeta_max_arr, a->zeta_max,
+                      a->cu_blocks, a->cu_blocks ? a->num_segments : 1, a->total_blocks,
+                      a->num_kv_heads, a->total_blocks,
+                      a->mask_out, a->active_out, a->indices, a->num_active,
+                      a->head_indices, a->head_num_active, a->head_uniform, a->empty_head_all};
+  return hip_check(oc::launch_compact(p, (hipStream_t)stream), "oc_mask_compact");
+}
+
+int oc_copy_blocks(const void* src, void* dst, const int32_t* indices, const int32_t* num_active,
+                   int32_t num_blocks, int64_t block_bytes, int32_t scatter, void* stream) {
+  if (!src || !dst || !indices || !num_active) return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (num_blocks < 0 || block_bytes <= 0 || block_bytes % 16 || !aligned16(src) || !aligned16(dst))
+    return fail(OC_ERR_INVALID_ARGUMENT, "blocks must be 16-byte aligned multiples of 16 bytes");
+  if (num_blocks > 65535) return fail(OC_ERR_UNSUPPORTED, "more than 65535 blocks");
+  oc::CopyParams p{src, dst, indices, num_active, num_blocks, block_bytes, scatter};
+  return hip_check(oc::launch_copy_blocks(p, (hipStream_t)stream), "oc_copy_blocks");
+}
+
+}  // extern "C"
+
+namespace {
+
+int make_attend_params(const oc_attend_args* a, oc::AttendParams& p) {
+  int rc = check_kv("k", a->k, a->kv_dtype, a->k_tok_stride, a->k_head_stride, a->head_dim);
+  if (rc) return rc;
+  rc = check_kv("v", a->v, a->kv_dtype, a->v_tok_stride, a->v_head_stride, a->head_dim);
+  if (rc) return rc;
+  if (!oc::attend_supported(a->kv_dtype, a->head_dim))
+    return fail(OC_ERR_UNSUPPORTED, "attention: head_dim %d unsupported for dtype %d", a->head_dim, a->kv_dtype);
+  if (!a->q || !a->out) return fail(OC_ERR_INVALID_ARGUMENT, "q or out is NULL");
+  if (!valid_dtype(a->q_dtype) || !valid_dtype(a->out_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "unknown dtype");
+  if (a->num_kv_heads <= 0 || a->group <= 0 || a->sq < 0 || a->block_size <= 0 || a->total_blocks < 0)
+    return fail(OC_ERR_INVALID_ARGUMENT, "bad shape");
+  const int nseg = a->cu_blocks ? a->num_segments : 1;
+  if (nseg <= 0) return fail(OC_ERR_INVALID_ARGUMENT, "num_segments must be > 0");
+  if ((int64_t)nseg * a->num_kv_heads > oc::kMaxLists)
+    return fail(OC_ERR_UNSUPPORTED, "segments x kv heads = %lld exceeds %d", (long long)nseg * a->num_kv_heads, oc::kMaxLists);
+  if (!a->indices || !a->counts) return fail(OC_ERR_INVALID_ARGUMENT, "indices/counts are NULL");
+  const int chunk = a->block_size < oc::kChunk ? a->block_size : oc::kChunk;
+  p = oc::AttendParams{};
+  p.q = a->q; p.q_dtype = a->q_dtype;
+  p.q_seg_stride = a->q_seg_stride; p.q_tok_stride = a->q_tok_stride; p.q_head_stride = a->q_head_stride;
+  p.k = a->k; p.v = a->v; p.kv_dtype = a->kv_dtype;
+  p.k_tok_stride = a->k_tok_stride; p.k_head_stride = a->k_head_stride;
+  p.v_tok_stride = a->v_tok_stride; p.v_head_stride = a->v_head_stride;
+  p.head_dim = a->head_dim; p.num_kv_heads = a->num_kv_heads; p.group = a->group; p.sq = a->sq;
+  p.block_size = a->block_size; p.total_blocks = a->total_blocks;
+  p.cu_blocks = a->cu_blocks; p.num_segments = nseg;
+  p.indices = a->indices; p.counts = a->counts; p.per_head = a->per_head; p.uniform = a->uniform;
+  p.logit_scale = (float)(1.4426950408889634 / std::sqrt((double)a->head_dim));
+  p.chunk = chunk; p.nchunk = (a->block_size + chunk - 1) / chunk;
+  p.part_o = nullptr; p.part_ml = nullptr;
+  p.out = a->out; p.out_dtype = a->out_dtype;
+  p.out_seg_stride = a->out_seg_stride; p.out_tok_stride = a->out_tok_stride; p.out_head_stride = a->out_head_stride;
+  return OC_OK;
+}
+
+size_t attend_ws(const oc::AttendParams& p) {
+  const int64_t items = oc::attend_max_items(p);
+  return align256((size_t)items * oc::kQG * p.head_dim * sizeof(float)) +
+         align256((size_t)items * oc::kQG * 2 * sizeof(float));
+}
+
+void attend_bind_ws(oc::AttendParams& p, void* ws) {
+  const int64_t items = oc::attend_max_items(p);
+  char* w = static_cast<char*>(ws);
+  p.part_o = reinterpret_cast<float*>(w);
+  p.part_ml = reinterpret_cast<float*>(w + align256((size_t)items * oc::kQG * p.head_dim * sizeof(float)));
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t oc_attend_workspace_size(const oc_attend_args* a) {
+  oc::AttendParams p;
+  if (!a || make_attend_params(a, p)) return 0;
+  return attend_ws(p);
+}
+
+int oc_attend(const oc_attend_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!a) return fail(OC_ERR_INVALID_ARGUMENT, "args is NULL");
+  oc::AttendParams p;
+  int rc = make_attend_params(a, p);
+  if (rc) return rc;
+  const size_t need = attend_ws(p);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(OC_ERR_WORKSPACE, "workspace %zu bytes < %zu needed", workspace_bytes, need);
+  attend_bind_ws(p, workspace);
+  return hip_check(oc::launch_attend(p, (hipStream_t)stream), "oc_attend");
+}
+
+}  // extern "C"
+
+namespace {
+
+struct LayerWs {
+  size_t tau, zeta, idx, cnt, attend, total;
+};
+
+LayerWs layer_ws_layout(const oc_layer_args* a, size_t attend_bytes) {
+  LayerWs w{};
+  const size_t tiles = (size_t)a->total_blocks * a->num_kv_heads;
+  const int nseg = a->cu_blocks ? a->num_segments : 1;
+  size_t off = 0;
+  w.tau = off; off += a->tau_max ? 0 : align256(tiles * 4);
+  w.zeta = off; off += a->zeta ? 0 : align256(tiles * 4);
+  w.idx = off; off += a->indices ? 0 : align256((size_t)a->total_blocks * 4);
+  w.cnt = off; off += a->num_active ? 0 : align256((size_t)nseg * 4);
+  w.attend = off; off += attend_bytes;
+  w.total = off;
+  return w;
+}
+
+oc_attend_args layer_attend_args(const oc_layer_args* a) {
+  oc_attend_args t{};
+  t.q = a->q; t.q_dtype = a->q_dtype;
+  t.q_seg_stride = a->q_seg_stride; t.q_tok_stride = a->q_tok_stride; t.q_head_stride = a->q_head_stride;
+  t.k = a->k; t.v = a->v; t.kv_dtype = a->kv_dtype;
+  t.k_tok_stride = a->k_tok_stride; t.k_head_stride = a->k_head_stride;
+  t.v_tok_stride = a->v_tok_stride; t.v_head_stride = a->v_head_stride;
+  t.head_dim = a->head_dim; t.num_kv_heads = a->num_kv_heads; t.group = a->group; t.sq = a->sq;
+  t.block_size = OC_BLOCK; t.total_blocks = a->total_blocks;
+  t.cu_blocks = a->cu_blocks; t.num_segments = a->num_segments;
+  t.indices = reinterpret_cast<const int32_t*>(16);  // placeholder: validated before binding
+  t.counts = reinterpret_cast<const int32_t*>(16);
+  t.per_head = 0; t.uniform = nullptr;
+  t.out = a->out; t.out_dtype = a->out_dtype;
+  t.out_seg_stride = a->out_seg_stride; t.out_tok_stride = a->out_tok_stride; t.out_head_stride = a->out_head_stride;
+  return t;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t oc_decode_layer_workspace_size(const oc_layer_args* a) {
+  if (!a) return 0;
+  oc_attend_args t = layer_attend_args(a);
+  oc::AttendParams p;
+  if (make_attend_params(&t, p)) return 0;
+  return layer_ws_layout(a, attend_ws(p)).total;
+}
+
+int oc_decode_layer(const oc_layer_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!a) return fail(OC_ERR_INVALID_ARGUMENT, "args is NULL");
+  oc_attend_args t = layer_attend_args(a);
+  oc::AttendParams ap;
+  int rc = make_attend_params(&t, ap);
+  if (rc) return rc;
+  if (!oc::score_supported(a->kv_dtype, a->head_dim))
+    return fail(OC_ERR_UNSUPPORTED, "scores: head_dim %d unsupported", a->head_dim);
+  const LayerWs w = layer_ws_layout(a, attend_ws(ap));
+  if (w.total && (!workspace || workspace_bytes < w.total))
+    return fail(OC_ERR_WORKSPACE, "workspace %zu bytes < %zu needed", workspace_bytes, w.total);
+  char* ws = static_cast<char*>(workspace);
+  float* tau_max = a->tau_max ? a->tau_max : reinterpret_cast<float*>(ws + w.tau);
+  float* zeta = a->zeta ? a->zeta : reinterpret_cast<float*>(ws + w.zeta);
+  int32_t* idx = a->indices ? a->indices : reinterpret_cast<int32_t*>(ws + w.idx);
+  int32_t* cnt = a->num_active ? a->num_active : reinterpret_cast<int32_t*>(ws + w.cnt);
+  const hipStream_t s = (hipStream_t)stream;
+
+  oc_score_args sa{};
+  sa.keys = a->k; sa.keys_dtype = a->kv_dtype;
+  sa.keys_tok_stride = a->k_tok_stride; sa.keys_head_stride = a->k_head_stride;
+  sa.head_dim = a->head_dim; sa.num_kv_heads = a->num_kv_heads; sa.total_blocks = a->total_blocks;
+  sa.cu_blocks = a->cu_blocks; sa.num_segments = a->num_segments;
+  sa.q = a->q; sa.q_dtype = a->q_dtype;
+  sa.q_seg_stride = a->q_seg_stride; sa.q_tok_stride = a->q_tok_stride; sa.q_head_stride = a->q_head_stride;
+  sa.sq = a->sq; sa.group = a->group;
+  sa.tau_max = tau_max; sa.zeta = zeta;
+  rc = oc_score_blocks(&sa, stream);
+  if (rc) return rc;
+
+  oc_compact_args ca{};
+  ca.tau_max = tau_max; ca.tau_parts = 1; ca.zeta = zeta;
+  ca.tau_arr = a->tau_arr; ca.tau = a->tau; ca.zeta_max_arr = a->zeta_max_arr; ca.zeta_max = a->zeta_max;
+  ca.cu_blocks = a->cu_blocks; ca.num_segments = a->num_segments;
+  ca.num_kv_heads = a->num_kv_heads; ca.total_blocks = a->total_blocks;
+  ca.mask_out = a->mask; ca.indices = idx; ca.num_active = cnt;
+  rc = oc_mask_compact(&ca, stream);
+  if (rc) return rc;
+
+  ap.indices = idx;
+  ap.counts = cnt;
+  attend_bind_ws(ap, ws + w.attend);
+  return hip_check(oc::launch_attend(ap, s), "oc_decode_layer attend");
+}
+
+}  // extern "C"

@@ -1,0 +1,142 @@
+// Shared device helpers for the OrthoCache gfx950 kernels.
+//
+// Element types: fp32, bf16 and fp16 inputs are loaded 16 bytes per lane
+// (global_load_dwordx4) and widened to fp32 in registers; all arithmetic on
+// the path is fp32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace oc {
+
+constexpr int kBlock = 512;          // tokens per KV block (the FWHT length)
+constexpr int kWave = 64;            // CDNA wavefront width
+constexpr float kSqrt512 = 22.627416997969522f;  // fp32 rounding of sqrt(512)
+
+enum DType : int { kF32 = 0, kBF16 = 1, kF16 = 2 };
+
+__host__ __device__ constexpr int dtype_size(int dt) { return dt == kF32 ? 4 : 2; }
+
+// ---------------------------------------------------------------- conversions
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);                       // round to nearest even
+  return u >> 16;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  return __half2float(__ushort_as_half(static_cast<unsigned short>(h & 0xffffu)));
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  return __half_as_ushort(__float2half_rn(f));
+}
+
+// Element type traits: VEC elements per 16-byte lane load.
+template <int DT> struct Elt;
+template <> struct Elt<kF32> {
+  static constexpr int VEC = 4;
+  __device__ __forceinline__ static void unpack(const uint4& w, float* o) {
+    o[0] = __uint_as_float(w.x); o[1] = __uint_as_float(w.y);
+    o[2] = __uint_as_float(w.z); o[3] = __uint_as_float(w.w);
+  }
+  __device__ __forceinline__ static float load1(const void* p, int64_t i) {
+    return reinterpret_cast<const float*>(p)[i];
+  }
+  __device__ __forceinline__ static void store1(void* p, int64_t i, float v) {
+    reinterpret_cast<float*>(p)[i] = v;
+  }
+};
+template <> struct Elt<kBF16> {
+  static constexpr int VEC = 8;
+  __device__ __forceinline__ static void unpack(const uint4& w, float* o) {
+    o[0] = bf16_lo(w.x); o[1] = bf16_hi(w.x); o[2] = bf16_lo(w.y); o[3] = bf16_hi(w.y);
+    o[4] = bf16_lo(w.z); o[5] = bf16_hi(w.z); o[6] = bf16_lo(w.w); o[7] = bf16_hi(w.w);
+  }
+  __device__ __forceinline__ static float load1(const void* p, int64_t i) {
+    return __uint_as_float(static_cast<uint32_t>(reinterpret_cast<const uint16_t*>(p)[i]) << 16);
+  }
+  __device__ __forceinline__ static void store1(void* p, int64_t i, float v) {
+    reinterpret_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+  }
+};
+template <> struct Elt<kF16> {
+  static constexpr int VEC = 8;
+  __device__ __forceinline__ static void unpack(const uint4& w, float* o) {
+    o[0] = f16_bits_to_f32(w.x); o[1] = f16_bits_to_f32(w.x >> 16);
+    o[2] = f16_bits_to_f32(w.y); o[3] = f16_bits_to_f32(w.y >> 16);
+    o[4] = f16_bits_to_f32(w.z); o[5] = f16_bits_to_f32(w.z >> 16);
+    o[6] = f16_bits_to_f32(w.w); o[7] = f16_bits_to_f32(w.w >> 16);
+  }
+  __device__ __forceinline__ static float load1(const void* p, int64_t i) {
+    return f16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+  }
+  __device__ __forceinline__ static void store1(void* p, int64_t i, float v) {
+    reinterpret_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(f32_to_f16_bits(v));
+  }
+};
+
+__device__ __forceinline__ float load_elt(int dt, const void* p, int64_t i) {
+  return dt == kF32 ? Elt<kF32>::load1(p, i) : (dt == kBF16 ? Elt<kBF16>::load1(p, i)
+                                                            : Elt<kF16>::load1(p, i));
+}
+__device__ __forceinline__ void store_elt(int dt, void* p, int64_t i, float v) {
+  if (dt == kF32) Elt<kF32>::store1(p, i, v);
+  else if (dt == kBF16) Elt<kBF16>::store1(p, i, v);
+  else Elt<kF16>::store1(p, i, v);
+}
+
+// 16-byte global load (the caller guarantees 16-byte alignment).
+__device__ __forceinline__ uint4 ld16(const void* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+
+// -------------------------------------------------------------- reductions
+// jnp.max semantics: NaN in either operand propagates.
+__device__ __forceinline__ float nanmax(float a, float b) { return (a > b || a != a) ? a : b; }
+
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WIDTH);
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<kWave>(v); }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Sum N values over the whole workgroup; every thread receives the totals.
+// lds must hold N * (blockDim.x / 64) floats.  Contains two barriers.
+template <int N>
+__device__ __forceinline__ void block_sum(float (&v)[N], float* lds) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nwaves = (blockDim.x + kWave - 1) / kWave;
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = wave_sum(v[i]);
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) lds[i * nwaves + wave] = v[i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    float s = 0.f;
+    for (int w = 0; w < nwaves; ++w) s += lds[i * nwaves + w];
+    v[i] = s;
+  }
+  __syncthreads();
+}
+
+}  // namespace oc

@@ -1,0 +1,156 @@
+// Internal kernel parameter blocks and launchers shared by the kernel
+// translation units and the C ABI (oc_api.hip).
+#pragma once
+
+#include "oc_common.h"
+
+namespace oc {
+
+// ------------------------------------------------------------ oc_fwht.hip
+struct FwhtParams {
+  const void* x;
+  int x_dtype;
+  int64_t x_batch_stride, x_row_stride;  // elements
+  void* y;
+  int y_dtype;
+  int64_t y_batch_stride, y_row_stride;
+  int64_t n_cols;
+  int64_t n_batch;
+};
+
+struct BandParams {
+  const float* spec;  // (nb, 512, H, D) fp32
+  int num_blocks, num_heads, head_dim;
+  int s0, s1;
+  float* out;
+};
+
+hipError_t launch_fwht(const FwhtParams& p, hipStream_t s);
+hipError_t launch_band_energy(const BandParams& p, hipStream_t s);
+
+// ----------------------------------------------------------- oc_score.hip
+struct ScoreParams {
+  const void* k;
+  int64_t k_tok_stride;   // elements between consecutive tokens
+  int64_t k_head_stride;  // elements between kv heads
+  int k_dtype;
+  int head_dim;
+  int num_kv_heads;
+  int total_blocks;
+  const int* cu_blocks;   // (num_segments + 1) block offsets, or null for one segment
+  int num_segments;
+  // Queries for the inline bound (may be null): segment s, query t, head hq
+  // at q + s*q_seg_stride + t*q_tok_stride + hq*q_head_stride.
+  const void* q;
+  int q_dtype;
+  int64_t q_seg_stride, q_tok_stride, q_head_stride;
+  int sq;      // queries per segment
+  int group;   // query heads per kv head
+  // Outputs, each optional.
+  float* tau_max;  // (total_blocks, Hkv): NaN-propagating max over queries
+  float* zeta;     // (total_blocks, Hkv)
+  float* dc;       // (total_blocks, Hkv, D): FWHT coefficient 0
+  float* e_low;
+  float* e_mid;
+  float* e_high;
+  float* e_ac;
+};
+
+struct BoundParams {
+  const float* dc;     // (nb, Hkv, D)
+  const float* e_ac;   // (nb, Hkv)
+  const void* q;
+  int q_dtype;
+  int64_t q_tok_stride, q_head_stride;
+  int sq, group, head_dim, num_kv_heads, num_blocks;
+  float* bounds;       // (sq*group, nb, Hkv) or null
+  float* tau_part;     // (ceil(sq*group/32), nb, Hkv) or null
+};
+
+struct EnergyParams {
+  const void* k;
+  int k_dtype;
+  int64_t k_tok_stride, k_head_stride;
+  int head_dim, num_kv_heads, num_blocks, block_size;
+  float* out;
+};
+
+bool score_supported(int dt, int head_dim);
+hipError_t launch_score(const ScoreParams& p, hipStream_t s);
+hipError_t launch_bound(const BoundParams& p, hipStream_t s);
+hipError_t launch_block_energy(const EnergyParams& p, hipStream_t s);
+
+// --------------------------------------------------------- oc_compact.hip
+struct CompactParams {
+  const float* tau_max;    // (tau_parts, total_blocks, Hkv)
+  int tau_parts;
+  const float* zeta;       // (total_blocks, Hkv) or null: gate 2 off
+  const uint8_t* mask_in;  // (total_blocks, mask_in_heads): use instead of scores when non-null
+  int mask_in_heads;
+  const float* tau_arr;    // per-segment thresholds, or null to use tau
+  float tau;
+  const float* zmax_arr;
+  float zeta_max;
+  const int* cu_blocks;    // (num_segments + 1) or null for one segment of nb_single blocks
+  int num_segments;
+  int nb_single;
+  int num_kv_heads;
+  int total_blocks;
+  uint8_t* mask_out;       // (total_blocks, Hkv) or null
+  uint8_t* active_out;     // (total_blocks) or null
+  int* indices;            // (total_blocks) or null: local block ids per segment
+  int* num_active;         // (num_segments) or null
+  int* head_indices;       // (Hkv, total_blocks) or null
+  int* head_num_active;    // (num_segments, Hkv)
+  uint8_t* head_uniform;   // (num_segments, Hkv) or null
+  int empty_head_all;
+};
+
+struct CopyParams {
+  const void* src;
+  void* dst;
+  const int* indices;
+  const int* num_active;
+  int num_blocks;
+  int64_t block_bytes;  // multiple of 16
+  int scatter;
+};
+
+hipError_t launch_compact(const CompactParams& p, hipStream_t s);
+hipError_t launch_copy_blocks(const CopyParams& p, hipStream_t s);
+
+// ---------------------------------------------------------- oc_attend.hip
+constexpr int kQG = 8;           // queries per attention work item
+constexpr int kMaxLists = 2048;  // (segments x kv heads) per launch
+constexpr int kChunk = 128;      // tokens per attention work item
+
+struct AttendParams {
+  const void* q;
+  int q_dtype;
+  int64_t q_seg_stride, q_tok_stride, q_head_stride;
+  const void* k;
+  const void* v;
+  int kv_dtype;
+  int64_t k_tok_stride, k_head_stride, v_tok_stride, v_head_stride;
+  int head_dim, num_kv_heads, group, sq;
+  int block_size, total_blocks;
+  const int* cu_blocks;  // (num_segments + 1) or null
+  int num_segments;
+  const int* indices;    // unified (total_blocks) or per head (Hkv, total_blocks)
+  const int* counts;     // unified (num_segments) or per head (num_segments, Hkv)
+  int per_head;
+  const uint8_t* uniform;  // (num_segments, Hkv) or null: equal weights on every token
+  float logit_scale;       // log2(e) / sqrt(head_dim)
+  int chunk, nchunk;
+  float* part_o;    // (max_items, kQG, D)
+  float* part_ml;   // (max_items, kQG, 2)
+  void* out;
+  int out_dtype;
+  int64_t out_seg_stride, out_tok_stride, out_head_stride;
+};
+
+bool attend_supported(int dt, int head_dim);
+int64_t attend_max_items(const AttendParams& p);
+hipError_t launch_attend(const AttendParams& p, hipStream_t s);
+
+}  // namespace oc

@@ -1,0 +1,228 @@
+"""GPU: the reference's end-to-end API (pipeline.py) and full-size configurations.
+
+Full-size runs are checked through properties that do not need the slow
+oracle: masks bit-exact against the oracle applied to the GPU's own fp32
+scores, the permutation's structure, scores of sampled blocks against the
+oracle, and attention against the float64 oracle over the retained blocks.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oc_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def np32(t):
+    return t.detach().float().cpu().numpy()
+
+
+def close(out, ref, rel):
+    out = np.asarray(out, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(out - ref).max() / max(np.abs(ref).max(), 1e-6)
+    assert err <= rel, f"max error {err:.3e} (tolerance {rel})"
+
+
+def tensors(dev, nb=4, sq=4, h=4, d=64, seed=42):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    return (torch.randn(sq, h, d, generator=g, device=dev), torch.randn(nb * 512, h, d, generator=g, device=dev),
+            torch.randn(nb * 512, h, d, generator=g, device=dev))
+
+
+class TestForward:
+    def test_dense_mode(self, dev):
+        import orthocache_amd as oc
+        from orthocache_amd.pipeline import _dense_attention
+
+        q, k, v = tensors(dev)
+        out, meta = oc.orthocache_forward(q, k, v, mode="dense")
+        assert out.shape == q.shape and meta["mode"] == "dense" and meta["eviction_rate"] == 0.0
+        assert "latency_ms" in meta and meta["num_blocks"] == 4 and meta["num_heads"] == 4 and meta["head_dim"] == 64
+        torch.testing.assert_close(out, _dense_attention(q, k, v, 64), atol=1e-5, rtol=1e-5)
+        close(np32(out), O.attention_active_blocks(np32(q), np32(k), np32(v), range(4)), 1e-4)
+
+    def test_invalid_mode(self, dev):
+        import orthocache_amd as oc
+
+        q, k, v = tensors(dev)
+        with pytest.raises(ValueError, match="Unknown mode"):
+            oc.orthocache_forward(q, k, v, mode="invalid")
+
+    @pytest.mark.parametrize("mode", ["sparse", "compact"])
+    def test_modes_metadata(self, dev, mode):
+        import orthocache_amd as oc
+
+        q, k, v = tensors(dev)
+        out, meta = oc.orthocache_forward(q, k, v, zeta_max=100.0, mode=mode)
+        assert out.shape == q.shape and meta["mode"] == mode
+        for key in ("zeta_mean", "zeta_std", "eviction_rate", "spectral_ms", "tau", "total_ms", "attention_ms",
+                    "blocks_retained", "blocks_evicted", "tau_auto"):
+            assert key in meta
+        if mode == "compact":
+            assert "compact_num_active" in meta
+        assert meta["total_ms"] >= 0
+
+    def test_compact_matches_oracle_end_to_end(self, dev):
+        import orthocache_amd as oc
+
+        q, k, v = tensors(dev, nb=8, sq=2, h=2, d=128, seed=7)
+        zeta = np32(oc.compute_spectral_decay_ratio(k))
+        tau = float(np.percentile(np32(oc.compute_query_aware_bounds(q, k)).max(axis=0), 60))
+        zmax = float(np.percentile(zeta, 90))
+        out, meta = oc.orthocache_forward(q, k, v, zeta_max=zmax, tau=tau, mode="compact")
+        from orthocache_amd import _ops
+
+        sc = _ops.score(k, q)
+        mask = O.mask_from_scores(np32(sc.tau_max).max(0), np32(sc.zeta), tau, zmax)
+        order, n = O.stream_compact_indices(mask)
+        assert meta["blocks_retained"] == n
+        ref = O.attention_active_blocks(np32(q), np32(k), np32(v), order[:n])
+        close(np32(out), ref, 1e-4)
+
+    def test_auto_tau(self, dev):
+        import orthocache_amd as oc
+        from orthocache_amd.pipeline import _compute_auto_tau
+
+        q, k, _ = tensors(dev, nb=6, sq=3, h=2, d=64, seed=11)
+        t = _compute_auto_tau(q, k)
+        ref = O.auto_tau(np32(q), np32(k))
+        assert math.isclose(t, ref, rel_tol=1e-4, abs_tol=1e-5)
+
+    def test_indirect_attention_meta(self, dev):
+        import orthocache_amd as oc
+
+        q, k, v = tensors(dev, nb=8, h=2)
+        m = torch.tensor([True, False] * 4, device=dev)[:, None].expand(8, 2)
+        out, meta = oc.indirect_attention(q, k, v, m)
+        assert meta["num_active"] == 4 and meta["bucket"] == 4 and meta["num_blocks"] == 8
+        assert 0.0 < meta["eviction_rate"] < 1.0
+        close(np32(out), O.attention_active_blocks(np32(q), np32(k), np32(v), [0, 2, 4, 6]), 1e-4)
+        out, meta = oc.indirect_attention(q, k, v, torch.zeros(8, 2, dtype=torch.bool, device=dev))
+        assert meta == {"num_active": 0, "bucket": 0, "eviction_rate": 1.0}
+        assert float(out.abs().sum()) == 0.0
+
+
+# ------------------------------------------------------------ full sizes
+def _check_layer(dev, wl, evict, sample_blocks=4):
+    """Score + compact + attend one layer at full size and check it."""
+    from orthocache_amd import _ops
+    from orthocache_amd.workloads import calibrate_unified
+
+    sc = _ops.score(wl.k, wl.q)
+    tau, zmax = calibrate_unified(sc.tau_max[0], sc.zeta, evict)
+    layer = _ops.DecodeLayer(wl.q, wl.k, wl.v, tau, zmax)
+    out = layer.run()
+    torch.cuda.synchronize()
+    nb = wl.k.shape[0] // 512
+    tm, z = np32(layer.tau_max), np32(layer.zeta)
+    # fused scores are the same kernel as the standalone scoring call
+    np.testing.assert_array_equal(tm, np32(sc.tau_max[0]))
+    mask = O.mask_from_scores(tm, z, tau, zmax)
+    order, n = O.stream_compact_indices(mask)
+    assert int(layer.num_active[0]) == n == int(round(nb * (1 - evict)))
+    np.testing.assert_array_equal(np32(layer.indices).astype(np.int64), order)
+    # scores of a few blocks against the float64 oracle
+    kk = wl.k.reshape(nb, 512, *wl.k.shape[1:])
+    qf = O.fold_gqa(np32(wl.q), wl.k.shape[1])
+    for b in np.linspace(0, nb - 1, sample_blocks).astype(int):
+        kb = np32(kk[b])
+        np.testing.assert_allclose(z[b], O.spectral_decay_ratio(kb)[0], rtol=1e-5)
+        np.testing.assert_allclose(tm[b], O.query_aware_bounds(qf, kb).max(axis=0)[0], rtol=1e-5, atol=1e-5)
+    # attention over the retained blocks, gathered on the device first
+    sel = torch.from_numpy(order[:n].astype(np.int64)).to(dev)
+    vv = wl.v.reshape(nb, 512, *wl.v.shape[1:])
+    k_act = kk.index_select(0, sel).reshape(n * 512, *wl.k.shape[1:])
+    v_act = vv.index_select(0, sel).reshape(n * 512, *wl.v.shape[1:])
+    ref = O.attention_active_blocks(np32(wl.q), np32(k_act), np32(v_act), range(n))
+    close(np32(out), ref, 1e-2)
+    return n
+
+
+@pytest.mark.parametrize("evict", [0.5, 0.75, 0.9])
+def test_c2_full_size(dev, evict):
+    from orthocache_amd import workloads
+
+    wl = workloads.c2(dev)
+    _check_layer(dev, wl, evict)
+
+
+def test_c1_config(dev):
+    from orthocache_amd import _ops, workloads
+
+    wl = workloads.c1(dev)
+    sc = _ops.score(wl.k, wl.q)
+    tm, z = sc.tau_max[0], sc.zeta
+    tau = workloads.percentile(tm, 50)
+    zmax = workloads.percentile(z, 75)
+    layer = _ops.DecodeLayer(wl.q, wl.k, wl.v, tau, zmax)
+    out = layer.run()
+    mask = O.mask_from_scores(np32(layer.tau_max), np32(layer.zeta), tau, zmax)
+    order, n = O.stream_compact_indices(mask)
+    np.testing.assert_array_equal(np32(layer.indices).astype(np.int64), order)
+    ref = O.attention_active_blocks(np32(wl.q), np32(wl.k), np32(wl.v), order[:n])
+    close(np32(out), ref, 1e-2)
+
+
+def test_c3_ragged(dev):
+    from orthocache_amd import varlen, workloads
+
+    wl = workloads.c3(dev)
+    cu = wl.cu_seqlens.cpu().numpy() // 512
+    tm, z = varlen.score_varlen(wl.q, wl.k, wl.cu_seqlens)
+    taus, zmaxs = [], []
+    for s in range(len(wl.meta["lens"])):
+        t, zm = workloads.calibrate_unified(tm[cu[s]:cu[s + 1]], z[cu[s]:cu[s + 1]], wl.meta["evict"][s])
+        taus.append(t)
+        zmaxs.append(zm)
+    tau_t = torch.tensor(taus, dtype=torch.float32, device=dev)
+    zmax_t = torch.tensor(zmaxs, dtype=torch.float32, device=dev)
+    out, meta = varlen.orthocache_decode_varlen(wl.q, wl.k, wl.v, wl.cu_seqlens, tau_t, zmax_t)
+    torch.cuda.synchronize()
+    idx = np32(meta["indices"]).astype(np.int64)
+    tmn, zn = np32(meta["tau_max"]), np32(meta["zeta"])
+    for s in range(len(wl.meta["lens"])):
+        lo, hi = cu[s], cu[s + 1]
+        mask = O.mask_from_scores(tmn[lo:hi], zn[lo:hi], taus[s], zmaxs[s])
+        order, n = O.stream_compact_indices(mask)
+        np.testing.assert_array_equal(idx[lo:hi], order)
+        assert int(meta["num_active"][s]) == n
+        if s % 8 == 0:
+            ref = O.attention_active_blocks(np32(wl.q[s]), np32(wl.k[lo * 512:hi * 512]),
+                                            np32(wl.v[lo * 512:hi * 512]), order[:n])
+            close(np32(out[s]), ref, 1e-2)
+
+
+def test_c5_sweep(dev):
+    from orthocache_amd import varlen, workloads
+
+    wl = workloads.c5(dev, sliding_layers=10, global_layers=2)  # same shapes per layer, fewer layers
+    cu = wl.cu_seqlens.cpu().numpy() // 512
+    tm, z = varlen.score_varlen(wl.q, wl.k, wl.cu_seqlens)
+    nl = len(wl.meta["lens"])
+    taus, zmaxs = [], []
+    for s in range(nl):
+        t, zm = workloads.calibrate_unified(tm[cu[s]:cu[s + 1]], z[cu[s]:cu[s + 1]], 0.9)
+        taus.append(t)
+        zmaxs.append(zm)
+    mask, idx, cnt = varlen.mask_compact_varlen(tm, z, wl.cu_seqlens, torch.tensor(taus, device=dev),
+                                                torch.tensor(zmaxs, device=dev))
+    torch.cuda.synchronize()
+    tmn, zn, idxn = np32(tm), np32(z), np32(idx).astype(np.int64)
+    for s in range(nl):
+        lo, hi = cu[s], cu[s + 1]
+        exp = O.mask_from_scores(tmn[lo:hi], zn[lo:hi], taus[s], zmaxs[s])
+        np.testing.assert_array_equal(np32(mask)[lo:hi].astype(bool), exp)
+        order, n = O.stream_compact_indices(exp)
+        np.testing.assert_array_equal(idxn[lo:hi], order)
+        assert int(cnt[s]) == n
+    # layer-0 scores vs the oracle
+    k0 = np32(wl.k[: cu[1] * 512])
+    q0 = O.fold_gqa(np32(wl.q[0]), 16)
+    np.testing.assert_allclose(zn[: cu[1]], O.spectral_decay_ratio(k0), rtol=1e-5)
+    np.testing.assert_allclose(tmn[: cu[1]], O.query_aware_bounds(q0, k0).max(axis=0), rtol=1e-5, atol=1e-5)

@@ -1,0 +1,138 @@
+"""CPU tests of the host side: the C-ABI library surface and the scoring identity.
+
+No GPU work is launched: the library is loaded, its exports are checked
+against include/orthocache_hip.h, and argument validation is exercised on
+NULL or malformed arguments (which fail before any device call).
+"""
+
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+from scipy.linalg import hadamard
+
+from oracle import oc_oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "orthocache_hip.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(oc_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from orthocache_amd import _native as N
+
+    if not N.LIB_PATH.exists():
+        pytest.fail("liborthocache_hip.so is not built: run __graft_entry__.build()")
+    return N.lib()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    syms = _declared_symbols()
+    assert len(syms) >= 14
+    missing = [s for s in syms if not hasattr(lib, s)]
+    assert missing == []
+
+
+def test_binding_covers_header(lib):
+    from orthocache_amd import _native as N
+
+    assert set(N.EXPORTED_SYMBOLS) == set(_declared_symbols())
+
+
+def test_abi_version(lib):
+    assert lib.oc_abi_version() == 1
+
+
+def test_struct_sizes_match_header_layout(lib):
+    # Field counts mirror the C structs; a mismatch would shift every field.
+    from orthocache_amd import _native as N
+
+    text = open(HEADER).read()
+    for cname, py in (("oc_fwht_args", N.FwhtArgs), ("oc_score_args", N.ScoreArgs),
+                      ("oc_bound_args", N.BoundArgs), ("oc_compact_args", N.CompactArgs),
+                      ("oc_attend_args", N.AttendArgs), ("oc_layer_args", N.LayerArgs)):
+        body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (cname, cname), text, re.S).group(1)
+        body = re.sub(r"/\*.*?\*/", "", body)
+        names = []
+        for decl in body.split(";"):
+            decl = decl.strip()
+            if not decl:
+                continue
+            decl = re.sub(r"^(const\s+)?[a-z0-9_]+\s*\**\s*", "", decl)
+            names += [n.strip().lstrip("*") for n in decl.split(",")]
+        assert names == [f[0] for f in py._fields_], cname
+
+
+def test_validation_errors_without_gpu(lib):
+    from orthocache_amd import _native as N
+
+    a = N.ScoreArgs()
+    assert lib.oc_score_blocks(C.byref(a), None) == -1
+    assert b"NULL" in lib.oc_last_error()
+    a.keys = 16
+    a.keys_dtype = 1
+    a.head_dim = 96  # 96 bf16 = 12 lanes of 8: not a supported layout
+    a.keys_tok_stride = 96
+    a.keys_head_stride = 96
+    a.num_kv_heads = 1
+    assert lib.oc_score_blocks(C.byref(a), None) == -2
+    assert b"head_dim" in lib.oc_last_error()
+    c = N.CompactArgs()
+    assert lib.oc_mask_compact(C.byref(c), None) == -1
+    assert lib.oc_copy_blocks(16, 16, 16, 16, 1, 100, 0, None) == -1  # not a multiple of 16
+    assert lib.oc_band_energy(16, 1, 1, 1, 10, 5, 16, None) == -1  # s0 > s1
+    assert lib.oc_query_bound_tiles(2, 16) == 1
+    assert lib.oc_query_bound_tiles(512, 1) == 16
+
+
+def test_attend_workspace_rejects_bad_args(lib):
+    from orthocache_amd import _native as N
+
+    a = N.AttendArgs()
+    assert lib.oc_attend_workspace_size(C.byref(a)) == 0
+    assert lib.oc_attend(C.byref(a), None, 0, None) == -1
+
+
+def _kernel_band_identity(block):
+    """NumPy emulation of the scoring kernel's arithmetic for one (512, D) tile:
+    bit-8 differences, a 4-point WHT over bits 6-7, and a centred low band."""
+    x = block.reshape(8, 64, -1)          # x[k, l, d] = K[64k + l, d]
+    d = x[:4] - x[4:]
+    e_high = 0.5 * np.sum(d * d)
+    u = x[:4] + x[4:]
+    a0, a1, a2, a3 = u[0] + u[1], u[0] - u[1], u[2] + u[3], u[2] - u[3]
+    y0, y1, y2, y3 = a0 + a2, a1 + a3, a0 - a2, a1 - a3
+    e_mid = 0.125 * np.sum(y1 * y1 + y2 * y2 + y3 * y3)
+    e_low = 0.125 * np.sum((y0 - y0.mean(axis=0, keepdims=True)) ** 2)
+    dc = y0.sum(axis=0) / np.sqrt(512)
+    return dc, e_low, e_mid, e_high
+
+
+@pytest.mark.parametrize("offset", [0.0, 5.0, 1e3])
+def test_scoring_identity_matches_full_spectrum(offset):
+    rng = np.random.default_rng(20)
+    blk = rng.standard_normal((512, 24)) + offset * rng.standard_normal(24)
+    dc, lo, mi, hi = _kernel_band_identity(blk)
+    c = hadamard(512) @ blk / np.sqrt(512)
+    np.testing.assert_allclose(dc, c[0], rtol=1e-12, atol=1e-9)
+    np.testing.assert_allclose(lo, np.sum(c[1:64] ** 2), rtol=1e-9)
+    np.testing.assert_allclose(mi, np.sum(c[64:256] ** 2), rtol=1e-9)
+    np.testing.assert_allclose(hi, np.sum(c[256:] ** 2), rtol=1e-9)
+
+
+def test_scoring_identity_fp32_cancellation_free():
+    # A large block mean must not swamp the low band (the centred form keeps
+    # it; E_0 - DC^2 in fp32 would lose it).
+    rng = np.random.default_rng(21)
+    blk = (rng.standard_normal((512, 64)) * 0.01 + 100.0).astype(np.float32)
+    _, lo32, _, _ = _kernel_band_identity(blk.astype(np.float32))
+    _, lo, _, _ = O.spectral_bands(blk.reshape(512, 1, 64).astype(np.float64))
+    np.testing.assert_allclose(lo32, lo[0, 0], rtol=1e-4)

@@ -1,0 +1,333 @@
+"""Pin the CPU oracle (oracle/oc_oracle.py) before trusting it.
+
+Checks come from outside the oracle's own formulas: the reference's
+published golden values (Gate 6), closed forms (Hadamard matrix, Parseval,
+bias-variance identity), brute force on tiny inputs, and the known answers
+of the reference's own tests, regenerated from their seeds.  The last tests
+plant typical mistakes in copies of oracle functions and confirm a check
+fails for each.
+"""
+
+import numpy as np
+import pytest
+from scipy.linalg import hadamard
+
+from oracle import oc_oracle as O
+
+H512 = hadamard(512).astype(np.float64)
+
+
+def gate6_blocks():
+    """Gate-6 inputs, built exactly as the reference notebook (cell 10)."""
+    n, nh, hd = 512, 4, 512
+    rng = np.random.RandomState(123)
+    a = np.zeros((n, nh, hd))
+    for h in range(nh):
+        for j in range(1, 16):
+            c = rng.randn(hd)
+            a[:, h, :] += np.outer(H512[:, j], c) / np.sqrt(n)
+    var_a = np.sum(a ** 2)
+    br = rng.randn(n, nh, hd)
+    b = br * np.sqrt(var_a / np.sum(br ** 2))
+    return a.astype(np.float32), b.astype(np.float32)
+
+
+# Reference golden values: benchmarks/results/orthocache_v4_31b_results.json:1387-1394
+GATE6_ZETA_A = 0.0
+GATE6_ZETA_B_MEAN = 4.037281036376953
+GATE6_AC_A = 7645.267578125
+GATE6_AC_B = 7629.59033203125
+
+
+class TestFWHT:
+    def test_closed_form_hadamard(self):
+        x = np.random.default_rng(0).standard_normal((512, 33))
+        np.testing.assert_allclose(O.fwht_512(x), H512 @ x / np.sqrt(512), rtol=0, atol=1e-12)
+
+    def test_reference_test_case(self):
+        # tests/test_fwht.py:8-20: 512x128 from np.random.seed(42), rtol/atol 1e-5
+        np.random.seed(42)
+        a = np.random.randn(512, 128).astype(np.float32)
+        np.testing.assert_allclose(O.fwht_512(a, dtype=np.float32), H512 @ a / np.sqrt(512), rtol=1e-5, atol=1e-5)
+
+    def test_1d(self):
+        x = np.random.default_rng(1).standard_normal(512)
+        y = O.fwht_512(x)
+        assert y.shape == (512,)
+        np.testing.assert_allclose(y, H512 @ x / np.sqrt(512), atol=1e-12)
+
+    def test_involution_and_parseval(self):
+        x = np.random.default_rng(2).standard_normal((512, 8))
+        y = O.fwht_512(x)
+        np.testing.assert_allclose(O.fwht_512(y), x, atol=1e-12)
+        np.testing.assert_allclose((y ** 2).sum(0), (x ** 2).sum(0), rtol=1e-12)
+
+    def test_known_answers(self):
+        const = np.ones(512)
+        y = O.fwht_512(const)
+        assert np.isclose(y[0], np.sqrt(512)) and np.allclose(y[1:], 0)
+        alt = np.where(np.arange(512) % 2 == 0, 1.0, -1.0)
+        y = O.fwht_512(alt)
+        assert np.isclose(y[1], np.sqrt(512)) and np.allclose(np.delete(y, 1), 0)
+        step = np.where(np.arange(512) < 256, 1.0, -1.0)
+        y = O.fwht_512(step)
+        assert np.isclose(y[256], np.sqrt(512)) and np.allclose(np.delete(y, 256), 0)
+
+    def test_blocks_layout(self):
+        rng = np.random.default_rng(3)
+        k = rng.standard_normal((1024, 3, 5))
+        spec = O.run_fwht_on_blocks(k)
+        assert spec.shape == (2, 512, 3, 5)
+        for b in range(2):
+            for h in range(3):
+                np.testing.assert_allclose(spec[b, :, h, :], H512 @ k[b * 512:(b + 1) * 512, h, :] / np.sqrt(512),
+                                           atol=1e-12)
+
+
+class TestBands:
+    def test_gate6_golden_fp32(self):
+        a, b = gate6_blocks()
+        za = O.spectral_decay_ratio(a, dtype=np.float32)
+        zb = O.spectral_decay_ratio(b, dtype=np.float32)
+        assert np.all(za == GATE6_ZETA_A)
+        # The fp32 restatement reproduces the published mean exactly.
+        assert float(np.mean(zb)) == GATE6_ZETA_B_MEAN
+        _, la, ma, ha = O.spectral_bands(a, dtype=np.float32)
+        _, lb, mb, hb = O.spectral_bands(b, dtype=np.float32)
+        assert float(np.mean(la + ma + ha)) == GATE6_AC_A
+        np.testing.assert_allclose(float(np.mean(lb + mb + hb)), GATE6_AC_B, rtol=1e-6)
+
+    def test_gate6_golden_fp64(self):
+        a, b = gate6_blocks()
+        np.testing.assert_allclose(np.mean(O.spectral_decay_ratio(b)), GATE6_ZETA_B_MEAN, rtol=1e-6)
+        assert np.all(np.abs(O.spectral_decay_ratio(a)) < 1e-20)
+
+    def test_brute_force_bands(self):
+        rng = np.random.default_rng(4)
+        k = rng.standard_normal((1024, 2, 7))
+        dc, lo, mi, hi = O.spectral_bands(k)
+        for b in range(2):
+            for h in range(2):
+                c = H512 @ k[b * 512:(b + 1) * 512, h, :] / np.sqrt(512)
+                np.testing.assert_allclose(dc[b, h], c[0], atol=1e-12)
+                np.testing.assert_allclose(lo[b, h], (c[1:64] ** 2).sum(), rtol=1e-12)
+                np.testing.assert_allclose(mi[b, h], (c[64:256] ** 2).sum(), rtol=1e-12)
+                np.testing.assert_allclose(hi[b, h], (c[256:] ** 2).sum(), rtol=1e-12)
+
+    def test_walsh_coherent_block(self):
+        # tests/test_spectral_bands.py:89-117
+        rng = np.random.RandomState(42)
+        blk = np.zeros((512, 64))
+        for j in range(1, 16):
+            w = np.ones(512)
+            for i in range(512):
+                for bit in range(9):
+                    if (j >> bit) & 1 and (i >> bit) & 1:
+                        w[i] *= -1
+            blk += np.outer(w, rng.randn(64) * 0.5)
+        z = O.spectral_decay_ratio(blk.reshape(512, 1, 64))
+        assert z[0, 0] < 0.01
+
+    def test_alternating_noise_block(self):
+        # tests/test_spectral_bands.py:70-86 (its assertion: zeta > 1)
+        np.random.seed(99)
+        blk = np.zeros((512, 64))
+        for i in range(512):
+            blk[i] = (1.0 if i % 2 == 0 else -1.0) * np.random.randn(64) * 2.0
+        assert O.spectral_decay_ratio(blk.reshape(512, 1, 64))[0, 0] > 1.0
+
+    def test_white_noise_expectation(self):
+        # E[zeta] -> 256/63 for white noise (high band 256 coefficients, low 63)
+        k = np.random.default_rng(5).standard_normal((512 * 64, 1, 64))
+        z = O.spectral_decay_ratio(k)
+        assert abs(np.mean(z) - 256 / 63) < 0.05
+
+    def test_block_energy_is_total_energy(self):
+        k = np.random.default_rng(6).standard_normal((1024, 4, 64))
+        dc, lo, mi, hi = O.spectral_bands(k)
+        np.testing.assert_allclose(O.block_energy(k), (dc ** 2).sum(-1) + lo + mi + hi, rtol=1e-12)
+
+
+class TestBounds:
+    def test_closed_form(self):
+        rng = np.random.default_rng(7)
+        q = rng.standard_normal((8, 4, 64))
+        k = rng.standard_normal((1024, 4, 64)) + 0.3
+        b = O.query_aware_bounds(q, k)
+        kb = k.reshape(2, 512, 4, 64)
+        kbar = kb.mean(axis=1)
+        eac = (kb ** 2).sum(axis=(1, 3)) - 512 * (kbar ** 2).sum(-1)
+        exp = (np.einsum("qhd,bhd->qbh", q, kbar) + np.linalg.norm(q, axis=-1)[:, None, :] * np.sqrt(eac)[None]) / 8.0
+        np.testing.assert_allclose(b, exp, rtol=1e-10)
+
+    def test_cauchy_schwarz_invariant(self):
+        rng = np.random.default_rng(8)
+        q = rng.standard_normal((5, 2, 32))
+        k = rng.standard_normal((1536, 2, 32))
+        b = O.query_aware_bounds(q, k)
+        logits = np.einsum("qhd,khd->qkh", q, k) / np.sqrt(32)
+        mx = logits.reshape(5, 3, 512, 2).max(axis=2)
+        assert np.all(b >= mx - 1e-9)
+
+    def test_gqa_fold(self):
+        rng = np.random.default_rng(9)
+        q = rng.standard_normal((3, 8, 16))  # 8 q heads over 2 kv heads
+        f = O.fold_gqa(q, 2)
+        assert f.shape == (12, 2, 16)
+        # query head h*G+g of token t lands on row t*G+g, kv head h
+        np.testing.assert_array_equal(f[1 * 4 + 3, 1], q[1, 1 * 4 + 3])
+
+
+class TestMasks:
+    def test_threshold_mask_kat(self):
+        # tests/test_energy.py:73-79
+        m = O.threshold_mask(np.array([[10.5, 2.3], [1.1, 15.6]]), 5.0)
+        np.testing.assert_array_equal(m, [[True, False], [False, True]])
+
+    def test_two_gate_reference_case(self):
+        # tests/test_spectral_bands.py:177-213 regenerated from its seed
+        np.random.seed(42)
+        keys = np.random.randn(1024, 1, 64).astype(np.float32)
+        for i in range(512):
+            keys[i, 0, :] *= (1.0 if i % 2 == 0 else -1.0) * 5.0
+        q = np.random.randn(1, 1, 64).astype(np.float32)
+        m = O.multiband_mask(q, keys, -100.0, 1.0)
+        assert m.shape == (2, 1) and not m.all()
+
+    def test_fp32_threshold_rounding_and_nan(self):
+        tau = 0.1  # not representable: JAX compares against fp32(0.1)
+        t32 = np.float32(tau)
+        scores = np.array([[t32, np.nextafter(t32, np.float32(0))], [np.nan, np.inf]], dtype=np.float32)
+        z = np.zeros_like(scores)
+        m = O.mask_from_scores(scores, z, tau, 1.0)
+        np.testing.assert_array_equal(m, [[True, False], [False, True]])
+        m = O.mask_from_scores(np.ones((1, 2), np.float32), np.array([[np.nan, 1.0]], np.float32), 0.0, 1.0)
+        np.testing.assert_array_equal(m, [[False, True]])
+
+    def test_nanmax_propagates(self):
+        x = np.array([[1.0, 2.0], [np.nan, 0.0]])
+        r = O.nanmax_axis0(x)
+        assert np.isnan(r[0]) and r[1] == 2.0
+
+
+class TestCompaction:
+    @pytest.mark.parametrize("mask,active", [
+        ([False, True, False, True, True, False], [1, 3, 4]),   # tests/test_alltoallv.py:60-67
+        ([True, False, True, True, False], [0, 2, 3]),          # tests/test_distributed.py:57-64
+        ([True, False, True, False, True, False, False, True], [0, 2, 4, 7]),  # test_adaptive_attention.py:60-67
+    ])
+    def test_known_answers(self, mask, active):
+        order, n = O.stream_compact_indices(np.array(mask))
+        assert n == len(active)
+        assert list(order[:n]) == active
+        assert sorted(order) == list(range(len(mask)))
+        assert list(order[n:]) == [i for i, m in enumerate(mask) if not m]
+
+    def test_all_and_none(self):
+        o, n = O.stream_compact_indices(np.ones(6, bool))
+        assert n == 6 and list(o) == list(range(6))
+        o, n = O.stream_compact_indices(np.zeros(6, bool))
+        assert n == 0 and list(o) == list(range(6))
+
+    def test_or_over_heads_and_brute_force(self):
+        rng = np.random.default_rng(10)
+        for nb in (1, 7, 64, 300):
+            m = rng.random((nb, 3)) < 0.2
+            o, n = O.stream_compact_indices(m)
+            act = m.any(1)
+            exp = [j for j in range(nb) if act[j]] + [j for j in range(nb) if not act[j]]
+            assert list(o) == exp and n == act.sum()
+
+    def test_exclusive_scan_kat(self):
+        off, tot = O.exclusive_scan([3, 2, 5, 1])  # tests/test_alltoallv.py:76-81
+        assert list(off) == [0, 3, 5, 10] and tot == 11
+
+    def test_compact_decompact_roundtrip(self):
+        rng = np.random.default_rng(11)
+        k = rng.standard_normal((4 * 512, 2, 8))
+        m = np.array([[True, False], [False, False], [False, True], [False, False]])
+        ck, cv, order, n = O.stream_compact(k, k, m)
+        assert n == 2 and np.all(ck[n:] == 0)
+        back = O.stream_decompact(ck, order, n, 4)
+        kb = k.reshape(4, 512, 2, 8)
+        np.testing.assert_array_equal(back[[0, 2]], kb[[0, 2]])
+        assert np.all(back[[1, 3]] == 0)
+
+
+class TestAttention:
+    def _data(self, nb=4, sq=2, hq=4, hkv=2, d=16, seed=12):
+        rng = np.random.default_rng(seed)
+        return (rng.standard_normal((sq, hq, d)), rng.standard_normal((nb * 512, hkv, d)),
+                rng.standard_normal((nb * 512, hkv, d)))
+
+    def test_all_blocks_equals_dense_softmax(self):
+        q, k, v = self._data()
+        out = O.attention_active_blocks(q, k, v, range(4))
+        g = 2
+        for h in range(4):
+            lg = q[:, h] @ k[:, h // g].T / 4.0
+            w = np.exp(lg - lg.max(1, keepdims=True))
+            w /= w.sum(1, keepdims=True)
+            np.testing.assert_allclose(out[:, h], w @ v[:, h // g], rtol=1e-12)
+
+    def test_online_loop_matches_closed_form(self):
+        q, k, v = self._data(nb=5, d=32)
+        order, n = O.stream_compact_indices(np.array([True, False, True, True, False]))
+        ref = O.attention_active_blocks(q, k, v, order[:n])
+        loop = O.online_softmax_loop_fp32(q, k, v, order, n)
+        np.testing.assert_allclose(loop, ref, rtol=2e-5, atol=2e-6)
+
+    def test_empty_gives_zeros(self):
+        q, k, v = self._data()
+        assert np.all(O.attention_active_blocks(q, k, v, []) == 0)
+        assert np.all(O.online_softmax_loop_fp32(q, k, v, np.arange(4), 0) == 0)
+
+    def test_per_head_semantics(self):
+        q, k, v = self._data(hq=2, hkv=2)
+        m = np.array([[True, False], [False, False], [True, False], [False, False]])
+        pred = O.attention_per_head_predicated(q, k, v, m)
+        gated = O.attention_per_head_gated(q, k, v, m)
+        np.testing.assert_allclose(pred[:, 0], O.attention_active_blocks(q[:, :1], k[:, :1], v[:, :1], [0, 2])[:, 0],
+                                   rtol=1e-10)
+        # head 1 keeps nothing: uniform weights -> mean of V; gated kernel -> zeros
+        np.testing.assert_allclose(pred[:, 1], np.broadcast_to(v[:, 1].mean(0), pred[:, 1].shape), rtol=1e-10)
+        assert np.all(gated[:, 1] == 0)
+
+
+class TestPlantedMistakes:
+    """Each plants a plausible oracle mistake and checks that a pin above catches it."""
+
+    def test_wrong_band_edge_fails_brute_force(self):
+        k = np.random.default_rng(13).standard_normal((512, 1, 8))
+        _, lo_bad, _, _ = O.spectral_bands(k, band_low=(0, 64))  # includes DC
+        c = H512 @ k[:, 0, :] / np.sqrt(512)
+        assert not np.isclose(lo_bad[0, 0], (c[1:64] ** 2).sum())
+
+    def test_missing_scale_fails_closed_form(self):
+        x = np.random.default_rng(14).standard_normal((512, 2))
+        bad = O.fwht_512(x) * np.sqrt(512)  # dropped 1/sqrt(512)
+        assert not np.allclose(bad, H512 @ x / np.sqrt(512))
+
+    def test_sequency_order_fails_known_answer(self):
+        # Reordering to sequency would move the alternating pattern to index 511.
+        alt = np.where(np.arange(512) % 2 == 0, 1.0, -1.0)
+        y = O.fwht_512(alt)
+        assert abs(y[511]) < 1e-9 and abs(y[1]) > 1
+
+    def test_unstable_partition_fails_kat(self):
+        m = np.array([False, True, False, True, True, False])
+        bad = np.argsort(-m.astype(int), kind="quicksort")
+        good, _ = O.stream_compact_indices(m)
+        # a non-stable sort need not give the reference order; the KAT pins it
+        assert list(good[:3]) == [1, 3, 4]
+        assert sorted(bad[:3]) == [1, 3, 4]
+
+    def test_wrong_sqrt_d_fails_closed_form(self):
+        rng = np.random.default_rng(15)
+        q = rng.standard_normal((2, 1, 16))
+        k = rng.standard_normal((512, 1, 16))
+        b = O.query_aware_bounds(q, k)
+        kbar = k.mean(0)
+        eac = (k ** 2).sum() - 512 * (kbar ** 2).sum()
+        wrong = (q[:, 0] @ kbar[0] + np.linalg.norm(q[:, 0], axis=-1) * np.sqrt(eac)) / 16.0  # d, not sqrt(d)
+        assert not np.allclose(b[:, 0, 0], wrong)
