@@ -162,7 +162,7 @@ typedef struct oc_compact_args {
   int32_t* num_active;     /* (num_segments) */
   int32_t* head_indices;   /* (Hkv, total_blocks) */
   int32_t* head_num_active;/* (num_segments, Hkv) */
-  uint8_t* head_uniform;   /* (num_segments, Hkv) */
+  int32_t* head_uniform;   /* (num_segments, Hkv) */
   int32_t empty_head_all;
 } oc_compact_args;
 int oc_mask_compact(const oc_compact_args* a, void* stream);
@@ -202,7 +202,7 @@ typedef struct oc_attend_args {
   const int32_t* indices;
   const int32_t* counts;
   int32_t per_head;
-  const uint8_t* uniform;
+  const int32_t* uniform;  /* (num_segments, Hkv), per-head lists only */
   void* out;
   int32_t out_dtype;
   int64_t out_seg_stride, out_tok_stride, out_head_stride;

@@ -26,10 +26,15 @@ def _kv_view(t: torch.Tensor, name: str) -> torch.Tensor:
     return t if ok else t.contiguous()
 
 
-def _q_view(t: torch.Tensor, name: str = "q") -> torch.Tensor:
-    if t.stride(-1) != 1:
-        t = t.contiguous()
-    return t
+def _q_view(t: torch.Tensor, kv_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Queries with unit dim stride and 16-byte aligned rows; with kv_dtype, in
+    the kv dtype or fp32 (the attention kernel reads one of the two)."""
+    if kv_dtype is not None and t.dtype not in (kv_dtype, torch.float32):
+        t = t.float()
+    es = t.element_size()
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all((t.stride(i) * es) % 16 == 0
+                                                             for i in range(t.dim() - 1) if t.shape[i] > 1)
+    return t if ok else t.clone(memory_format=torch.contiguous_format)
 
 
 def kv_group(q_heads: int, kv_heads: int) -> int:
@@ -114,7 +119,7 @@ def score(keys: torch.Tensor, q: torch.Tensor | None = None, *, want_bands: bool
     sq = group = 0
     q_ok = q is not None
     if q_ok:
-        q = _q_view(q)
+        q = _q_view(q, keys.dtype)
         if cu_blocks is None:
             if q.dim() != 3:
                 raise ValueError("q must be (seq_q, heads, head_dim)")
@@ -176,7 +181,7 @@ class Compacted:
     num_active: torch.Tensor | None    # (segments,) int32
     head_indices: torch.Tensor | None = None     # (Hkv, nb) int32
     head_num_active: torch.Tensor | None = None  # (segments, Hkv) int32
-    head_uniform: torch.Tensor | None = None     # (segments, Hkv) uint8
+    head_uniform: torch.Tensor | None = None     # (segments, Hkv) int32
 
 
 def mask_compact(*, num_blocks: int, num_kv_heads: int, device: torch.device,
@@ -242,7 +247,7 @@ def mask_compact(*, num_blocks: int, num_kv_heads: int, device: torch.device,
     if want_head_lists:
         res.head_indices = torch.empty((hkv, nb), **i32)
         res.head_num_active = torch.empty((num_segments, hkv), **i32)
-        res.head_uniform = torch.empty((num_segments, hkv), **u8)
+        res.head_uniform = torch.empty((num_segments, hkv), **i32)
         a.head_indices = ptr(res.head_indices); a.head_num_active = ptr(res.head_num_active)
         a.head_uniform = ptr(res.head_uniform); a.empty_head_all = 1 if empty_head_all else 0
     check(lib().oc_mask_compact(C.byref(a), stream_ptr(device)), "oc_mask_compact")
@@ -268,9 +273,10 @@ def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, indices: torch.Ten
     """Attention over the listed blocks.  q: (Sq, Hq, D) (or (B, Sq, Hq, D) with
     cu_blocks); k, v: (S, Hkv, D).  Returns q-shaped output in out_dtype."""
     require_gpu(q, k, v, indices, counts)
+    out_dtype = out_dtype or q.dtype
     k = _kv_view(k, "keys")
     v = _kv_view(v, "values")
-    q = _q_view(q)
+    q = _q_view(q, k.dtype)
     s, hkv, d = k.shape
     if v.shape != k.shape:
         raise ValueError(f"values shape {tuple(v.shape)} != keys shape {tuple(k.shape)}")
@@ -281,7 +287,7 @@ def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, indices: torch.Ten
     group = kv_group(q.shape[-2], hkv)
     sq = q.shape[-3]
     if out is None:
-        out = torch.empty(q.shape, dtype=out_dtype or q.dtype, device=q.device)
+        out = torch.empty(q.shape, dtype=out_dtype, device=q.device)
     a = N.AttendArgs()
     a.q = ptr(q); a.q_dtype = dtype_code(q.dtype)
     a.q_seg_stride = q.stride(0) if q.dim() == 4 else 0
@@ -323,7 +329,7 @@ class DecodeLayer:
         require_gpu(q, k, v, cu_blocks)
         self.k = _kv_view(k, "keys")
         self.v = _kv_view(v, "values")
-        self.q = _q_view(q)
+        self.q = _q_view(q, self.k.dtype)
         s, hkv, d = self.k.shape
         if s % BLOCK:
             raise ValueError(f"seq_len {s} is not a multiple of {BLOCK}")
@@ -331,7 +337,7 @@ class DecodeLayer:
         dev = self.k.device
         self.device = dev
         group = kv_group(self.q.shape[-2], hkv)
-        self.out = out if out is not None else torch.empty(self.q.shape, dtype=out_dtype or self.q.dtype, device=dev)
+        self.out = out if out is not None else torch.empty(self.q.shape, dtype=out_dtype or q.dtype, device=dev)
         f32 = dict(dtype=torch.float32, device=dev)
         self.tau_max = torch.empty((nb, hkv), **f32) if keep_scores else None
         self.zeta = torch.empty((nb, hkv), **f32) if keep_scores else None

@@ -93,7 +93,11 @@ int oc_score_blocks(const oc_score_args* a, void* stream) {
   if (a->cu_blocks && a->num_segments <= 0) return fail(OC_ERR_INVALID_ARGUMENT, "cu_blocks needs num_segments > 0");
   if (a->q) {
     if (!valid_dtype(a->q_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "q: unknown dtype");
+    if (a->q_dtype != a->keys_dtype && a->q_dtype != OC_F32)
+      return fail(OC_ERR_UNSUPPORTED, "q dtype must equal the key dtype or be fp32");
     if (a->sq < 0 || a->group <= 0) return fail(OC_ERR_INVALID_ARGUMENT, "bad sq/group");
+    if (a->cu_blocks && a->num_segments > 4096)
+      return fail(OC_ERR_UNSUPPORTED, "at most 4096 segments per call");
   }
   oc::ScoreParams p{a->keys, a->keys_tok_stride, a->keys_head_stride, a->keys_dtype, a->head_dim,
                     a->num_kv_heads, a->total_blocks, a->cu_blocks, a->cu_blocks ? a->num_segments : 1,
@@ -122,7 +126,8 @@ int oc_mask_compact(const oc_compact_args* a, void* stream) {
   if (!a->mask_in && !a->tau_max) return fail(OC_ERR_INVALID_ARGUMENT, "need tau_max or mask_in");
   if (a->mask_in && a->mask_in_heads != 1 && a->mask_in_heads != a->num_kv_heads)
     return fail(OC_ERR_INVALID_ARGUMENT, "mask_in_heads must be 1 or num_kv_heads");
-  if (a->num_kv_heads <= 0 || a->total_blocks < 0) return fail(OC_ERR_INVALID_ARGUMENT, "bad shape");
+  if (a->num_kv_heads <= 0 || a->num_kv_heads > 16384 || a->total_blocks < 0)
+    return fail(OC_ERR_INVALID_ARGUMENT, "bad shape");
   if (a->tau_max && a->tau_parts <= 0) return fail(OC_ERR_INVALID_ARGUMENT, "tau_parts must be > 0");
   if (a->cu_blocks && a->num_segments <= 0) return fail(OC_ERR_INVALID_ARGUMENT, "cu_blocks needs num_segments > 0");
   if (a->indices && !a->num_active) return fail(OC_ERR_INVALID_ARGUMENT, "indices needs num_active");
@@ -159,6 +164,13 @@ int make_attend_params(const oc_attend_args* a, oc::AttendParams& p) {
     return fail(OC_ERR_UNSUPPORTED, "attention: head_dim %d unsupported for dtype %d", a->head_dim, a->kv_dtype);
   if (!a->q || !a->out) return fail(OC_ERR_INVALID_ARGUMENT, "q or out is NULL");
   if (!valid_dtype(a->q_dtype) || !valid_dtype(a->out_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "unknown dtype");
+  if (a->q_dtype != a->kv_dtype && a->q_dtype != OC_F32)
+    return fail(OC_ERR_UNSUPPORTED, "q dtype must equal the kv dtype or be fp32");
+  {
+    const int qs = esize(a->q_dtype);
+    if (!aligned16(a->q) || (a->q_tok_stride * qs) % 16 || (a->q_head_stride * qs) % 16 || (a->q_seg_stride * qs) % 16)
+      return fail(OC_ERR_INVALID_ARGUMENT, "q must be 16-byte aligned with 16-byte multiple strides");
+  }
   if (a->num_kv_heads <= 0 || a->group <= 0 || a->sq < 0 || a->block_size <= 0 || a->total_blocks < 0)
     return fail(OC_ERR_INVALID_ARGUMENT, "bad shape");
   const int nseg = a->cu_blocks ? a->num_segments : 1;
@@ -166,7 +178,7 @@ int make_attend_params(const oc_attend_args* a, oc::AttendParams& p) {
   if ((int64_t)nseg * a->num_kv_heads > oc::kMaxLists)
     return fail(OC_ERR_UNSUPPORTED, "segments x kv heads = %lld exceeds %d", (long long)nseg * a->num_kv_heads, oc::kMaxLists);
   if (!a->indices || !a->counts) return fail(OC_ERR_INVALID_ARGUMENT, "indices/counts are NULL");
-  const int chunk = a->block_size < oc::kChunk ? a->block_size : oc::kChunk;
+  const int chunk = oc::attend_chunk(a->kv_dtype, a->head_dim, a->sq * a->group);
   p = oc::AttendParams{};
   p.q = a->q; p.q_dtype = a->q_dtype;
   p.q_seg_stride = a->q_seg_stride; p.q_tok_stride = a->q_tok_stride; p.q_head_stride = a->q_head_stride;

@@ -13,48 +13,75 @@
 // the device; every workgroup derives the work-item space from them, so no
 // host synchronisation or recompilation is needed when the count changes.
 //
-// Work item = (list, slot i < count, chunk of `chunk` tokens, query group of
-// up to 8 queries).  A workgroup streams the chunk's K and V rows once
-// (16-byte lane loads, LPR lanes per row), keeps per-row-slot online-softmax
-// state (m, l, o) for its queries, merges the slots in LDS and writes one
-// partial (m, l, o[D]).  combine_kernel merges the partials of a list in a
-// fixed order (log-sum-exp), so results are deterministic.
+// Work item = (list, slot i < count, chunk of tokens, query group of up to 8
+// queries).  A workgroup (256 threads) takes one item:
+//   - LPR lanes per token row (16-byte loads along head_dim, coalesced),
+//     NSLOT = 256/LPR row slots, R rows per slot; every K and V row of the
+//     item is requested before any arithmetic, so one HBM round trip covers
+//     the item;
+//   - the R x NQ partial dot products of a lane are reduced across its LPR
+//     lanes with a halving butterfly (V - 1 shuffles for V values instead of
+//     V log2(LPR)), leaving each lane one logit;
+//   - per-slot softmax from LDS, P.V in registers, slots merged by shuffles
+//     inside a wave and through LDS across waves; one partial (m, l, o[D]).
+// combine_kernel merges a list's partials in item order (log-sum-exp), so the
+// result is deterministic.
 //
 // Logits are kept in the log2 domain: s2 = q.k * log2(e) / sqrt(d), weights
-// exp2(s2 - m2); the result is identical in exact arithmetic.
+// exp2(s2 - m2); identical to the natural-log form in exact arithmetic.
 #include "oc_kernels.h"
 
 namespace oc {
-
 
 __device__ __forceinline__ int list_count(const AttendParams& p, int list) {
   if (p.per_head) return p.counts[list];
   return p.counts[list / p.num_kv_heads];
 }
 
-// Exclusive prefix over lists of items per list into s_off[0..nlists].
-__device__ int build_item_offsets(const AttendParams& p, int* s_off, int nqg) {
-  const int nlists = p.num_segments * p.num_kv_heads;
-  const int t = threadIdx.x;
-  // Serial scan per thread over a contiguous range, then a scan of range totals.
-  __shared__ int s_part[256];
-  const int per = (nlists + blockDim.x - 1) / blockDim.x;
-  const int lo = t * per;
-  const int hi = min(lo + per, nlists);
-  int sum = 0;
-  for (int i = lo; i < hi; ++i) sum += list_count(p, i) * p.nchunk * nqg;
-  s_part[t] = sum;
+// Exclusive scan of one int per thread over a 256-thread workgroup.
+__device__ __forceinline__ int block_exclusive_scan(int v, int* s_wave, int& total) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int u = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += u;
+  }
+  if (lane == kWave - 1) s_wave[wave] = incl;
   __syncthreads();
-  if (t == 0) {
-    int run = 0;
-    for (int i = 0; i < (int)blockDim.x; ++i) { const int c = s_part[i]; s_part[i] = run; run += c; }
-    s_off[nlists] = run;
+  int before = 0, tot = 0;
+  const int nw = blockDim.x / kWave;
+  for (int w = 0; w < nw; ++w) {
+    const int c = s_wave[w];
+    before += (w < wave) ? c : 0;
+    tot += c;
   }
   __syncthreads();
-  int run = s_part[t];
-  for (int i = lo; i < hi; ++i) { s_off[i] = run; run += list_count(p, i) * p.nchunk * nqg; }
+  total = tot;
+  return before + incl - v;
+}
+
+// s_off[list] = first item of the list, s_off[nlists] = total items.
+__device__ int build_item_offsets(const AttendParams& p, int* s_off, int nqg) {
+  __shared__ int s_wave[8];
+  const int nlists = p.num_segments * p.num_kv_heads;
+  const int t = threadIdx.x;
+  const int per = (nlists + blockDim.x - 1) / blockDim.x;
+  const int lo = min(t * per, nlists);
+  const int hi = min(lo + per, nlists);
+  const int mult = p.nchunk * nqg;
+  int sum = 0;
+  for (int i = lo; i < hi; ++i) sum += list_count(p, i) * mult;
+  int total;
+  int run = block_exclusive_scan(sum, s_wave, total);
+  for (int i = lo; i < hi; ++i) {
+    s_off[i] = run;
+    run += list_count(p, i) * mult;
+  }
+  if (t == 0) s_off[nlists] = total;
   __syncthreads();
-  return s_off[nlists];
+  return total;
 }
 
 __device__ __forceinline__ int find_list(const int* s_off, int nlists, int item) {
@@ -66,67 +93,82 @@ __device__ __forceinline__ int find_list(const int* s_off, int nlists, int item)
   return lo;
 }
 
-template <int DT, int LPR, int NQ>
+// Halving butterfly over LPR lanes.  With V >= LPR, lane l ends with the full
+// sums of value indices [l*V/LPR, (l+1)*V/LPR) in v[0..V/LPR); with V < LPR,
+// v[0] of lane l is the sum of index l / (LPR/V).
+template <int V, int CNT, int B, int LPR>
+struct Butterfly {
+  __device__ __forceinline__ static void run(float (&v)[V], int lane) {
+    if constexpr (B >= 1) {
+      if constexpr (CNT > 1) {
+        constexpr int H = CNT / 2;
+        const bool upper = (lane & B) != 0;
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+          const float send = upper ? v[i] : v[i + H];
+          const float keep = upper ? v[i + H] : v[i];
+          v[i] = keep + __shfl_xor(send, B, LPR);
+        }
+        Butterfly<V, H, B / 2, LPR>::run(v, lane);
+      } else {
+        v[0] += __shfl_xor(v[0], B, LPR);
+        Butterfly<V, 1, B / 2, LPR>::run(v, lane);
+      }
+    }
+  }
+};
+
+template <int NQ>
+__host__ __device__ constexpr int rows_per_slot() {
+  return NQ <= 4 ? 8 : 4;
+}
+
+template <int DT, int LPR, int NQ, int QDT>
 __global__ __launch_bounds__(256) void attend_decode_kernel(AttendParams p) {
   using E = Elt<DT>;
+  using EQ = Elt<QDT>;
   constexpr int VEC = E::VEC;
   constexpr int D = LPR * VEC;
   constexpr int NSLOT = 256 / LPR;
   constexpr int ESZ = (DT == kF32) ? 4 : 2;
-  constexpr int RB = 4;  // rows per sub-batch per slot
+  constexpr int R = rows_per_slot<NQ>();
+  constexpr int V = R * NQ;                       // logits per slot
+  constexpr int PER_LANE = V >= LPR ? V / LPR : 1;
+  constexpr int SPW = kWave / LPR;                // slots per wave
+  constexpr int NWAVE = 256 / kWave;
 
   __shared__ int s_off[kMaxLists + 1];
-  __shared__ float s_o[NSLOT * NQ * D];
-  __shared__ float s_m[NSLOT * NQ];
-  __shared__ float s_l[NSLOT * NQ];
+  __shared__ float s_log[NSLOT * V];
+  __shared__ float s_o[NWAVE * NQ * D];
+  __shared__ float s_m[NWAVE * NQ];
+  __shared__ float s_l[NWAVE * NQ];
 
   const int nq_total = p.sq * p.group;
   const int nqg = (nq_total + kQG - 1) / kQG;
   const int nlists = p.num_segments * p.num_kv_heads;
-  const int total_items = build_item_offsets(p, s_off, nqg);
+  // One segment with one list shared by the heads: every list has the same
+  // length, so no prefix is needed.
+  const bool uniform_lists = !p.per_head && p.num_segments == 1;
+  const int ipl = uniform_lists ? p.counts[0] * p.nchunk * nqg : 0;
+  const int total_items = uniform_lists ? ipl * nlists : build_item_offsets(p, s_off, nqg);
 
   const int t = threadIdx.x;
   const int cc = t % LPR;
   const int slot = t / LPR;
-  const int rows_per_slot = (p.chunk + NSLOT - 1) / NSLOT;
+  const int wave = t / kWave;
 
   for (int item = blockIdx.x; item < total_items; item += gridDim.x) {
-    const int list = find_list(s_off, nlists, item);
-    int r = item - s_off[list];
-    const int qg = r % nqg; r /= nqg;
-    const int c = r % p.nchunk;
-    const int i = r / p.nchunk;
+    const int list = uniform_lists ? item / ipl : find_list(s_off, nlists, item);
+    int r0 = item - (uniform_lists ? list * ipl : s_off[list]);
+    const int qg = r0 % nqg; r0 /= nqg;
+    const int c = r0 % p.nchunk;
+    const int i = r0 / p.nchunk;
     const int seg = list / p.num_kv_heads;
     const int h = list - seg * p.num_kv_heads;
     const int off = p.cu_blocks ? p.cu_blocks[seg] : 0;
     const int blk = p.indices[(p.per_head ? (int64_t)h * p.total_blocks : 0) + off + i];
-    const bool uni = p.uniform && p.uniform[list];
     const int64_t tok0 = (int64_t)(off + blk) * p.block_size + (int64_t)c * p.chunk;
     const int nrows = min(p.chunk, p.block_size - c * p.chunk);
-
-    // Queries of this item (NQ slots; missing ones are zero and ignored).
-    float qv[NQ][VEC];
-#pragma unroll
-    for (int g = 0; g < NQ; ++g) {
-      const int qi = qg * kQG + g;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) qv[g][e] = 0.f;
-      if (qi < nq_total) {
-        const int st = qi / p.group, gg = qi - st * p.group;
-        const int64_t qo = (int64_t)seg * p.q_seg_stride + (int64_t)st * p.q_tok_stride +
-                           (int64_t)(h * p.group + gg) * p.q_head_stride + cc * VEC;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) qv[g][e] = load_elt(p.q_dtype, p.q, qo + e) * p.logit_scale;
-      }
-    }
-
-    float m[NQ], l[NQ], o[NQ][VEC];
-#pragma unroll
-    for (int g = 0; g < NQ; ++g) {
-      m[g] = -INFINITY; l[g] = 0.f;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) o[g][e] = 0.f;
-    }
 
     const char* kb = reinterpret_cast<const char*>(p.k) +
                      (tok0 * p.k_tok_stride + (int64_t)h * p.k_head_stride + (int64_t)cc * VEC) * ESZ;
@@ -134,103 +176,172 @@ __global__ __launch_bounds__(256) void attend_decode_kernel(AttendParams p) {
                      (tok0 * p.v_tok_stride + (int64_t)h * p.v_head_stride + (int64_t)cc * VEC) * ESZ;
     const int64_t krow = p.k_tok_stride * ESZ, vrow = p.v_tok_stride * ESZ;
 
-    for (int r0 = 0; r0 < rows_per_slot; r0 += RB) {
-      uint4 kw[RB], vw[RB];
-      bool ok[RB];
+    // Issue every K and V load of this item first.  Row indices are clamped
+    // into the block (loads stay unconditional, so none waits behind a
+    // branch) and rows past nrows are masked afterwards.
+    uint4 kw[R], vw[R];
 #pragma unroll
-      for (int u = 0; u < RB; ++u) {
-        const int row = slot + NSLOT * (r0 + u);
-        ok[u] = (r0 + u < rows_per_slot) && (row < nrows);
-        if (ok[u]) {
-          kw[u] = ld16(kb + row * krow);
-          vw[u] = ld16(vb + row * vrow);
-        }
-      }
-      float s[RB][NQ];
+    for (int r = 0; r < R; ++r) kw[r] = ld16(kb + min(slot + NSLOT * r, nrows - 1) * krow);
 #pragma unroll
-      for (int u = 0; u < RB; ++u) {
-        float kx[VEC];
-        if (ok[u]) E::unpack(kw[u], kx);
+    for (int r = 0; r < R; ++r) vw[r] = ld16(vb + min(slot + NSLOT * r, nrows - 1) * vrow);
+
+    // Queries (pre-scaled by log2(e)/sqrt(d)); 16-byte loads of the lane's
+    // VEC elements, query index clamped and missing queries zeroed.
+    float qv[NQ][VEC];
 #pragma unroll
-        for (int g = 0; g < NQ; ++g) {
-          float d = 0.f;
-          if (ok[u]) {
+    for (int g = 0; g < NQ; ++g) {
+      const int qi = qg * kQG + g;
+      const int qc = min(qi, nq_total - 1);
+      const int st = qc / p.group, gg = qc - st * p.group;
+      constexpr int QSZ = (QDT == kF32) ? 4 : 2;
+      const char* qp = reinterpret_cast<const char*>(p.q) +
+                       ((int64_t)seg * p.q_seg_stride + (int64_t)st * p.q_tok_stride +
+                        (int64_t)(h * p.group + gg) * p.q_head_stride + (int64_t)cc * VEC) * QSZ;
+      const float sc = qi < nq_total ? p.logit_scale : 0.f;
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) d = fmaf(qv[g][e], kx[e], d);
-          }
-          d = group_sum<LPR>(d);
-          s[u][g] = ok[u] ? (uni ? 0.f : d) : -INFINITY;
-        }
-      }
+      for (int e0 = 0; e0 < VEC; e0 += EQ::VEC) {
+        float tmp[EQ::VEC];
+        EQ::unpack(ld16(qp + e0 * QSZ), tmp);
 #pragma unroll
-      for (int g = 0; g < NQ; ++g) {
-        float mb = s[0][g];
-#pragma unroll
-        for (int u = 1; u < RB; ++u) mb = fmaxf(mb, s[u][g]);
-        const float mn = fmaxf(m[g], mb);
-        if (mn == -INFINITY) continue;  // nothing valid yet in this slot
-        const float alpha = exp2f(m[g] - mn);
-        float pw[RB];
-        float ls = 0.f;
-#pragma unroll
-        for (int u = 0; u < RB; ++u) { pw[u] = exp2f(s[u][g] - mn); ls += pw[u]; }
-        l[g] = l[g] * alpha + ls;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) o[g][e] *= alpha;
-#pragma unroll
-        for (int u = 0; u < RB; ++u) {
-          if (ok[u]) {
-            float vx[VEC];
-            E::unpack(vw[u], vx);
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) o[g][e] = fmaf(pw[u], vx[e], o[g][e]);
-          }
-        }
-        m[g] = mn;
+        for (int e = 0; e < EQ::VEC && e0 + e < VEC; ++e) qv[g][e0 + e] = tmp[e] * sc;
       }
     }
 
-    // Merge the NSLOT row slots.
+    // Uniform per workgroup: a scalar load, which does not wait on the K/V loads.
+    const bool uni = (p.uniform != nullptr) && (p.uniform[list] != 0);
+
+    // Partial dot products, value index r*NQ + g.
+    float part[V];
 #pragma unroll
-    for (int g = 0; g < NQ; ++g) {
+    for (int r = 0; r < R; ++r) {
+      float kx[VEC];
+      E::unpack(kw[r], kx);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) s_o[(slot * NQ + g) * D + cc * VEC + e] = o[g][e];
-      if (cc == 0) { s_m[slot * NQ + g] = m[g]; s_l[slot * NQ + g] = l[g]; }
+      for (int g = 0; g < NQ; ++g) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) d = fmaf(qv[g][e], kx[e], d);
+        part[r * NQ + g] = d;
+      }
+    }
+    Butterfly<V, V, LPR / 2, LPR>::run(part, cc);
+
+    // Logits to LDS (invalid rows -inf, uniform lists 0).
+    if constexpr (V >= LPR) {
+#pragma unroll
+      for (int u = 0; u < PER_LANE; ++u) {
+        const int idx = cc * PER_LANE + u;
+        const int row = slot + NSLOT * (idx / NQ);
+        s_log[slot * V + idx] = row < nrows ? (uni ? 0.f : part[u]) : -INFINITY;
+      }
+    } else {
+      constexpr int REP = LPR / V;
+      if (cc % REP == 0) {
+        const int idx = cc / REP;
+        const int row = slot + NSLOT * (idx / NQ);
+        s_log[slot * V + idx] = row < nrows ? (uni ? 0.f : part[0]) : -INFINITY;
+      }
     }
     __syncthreads();
+
+    // Per-slot softmax state and P.V.
+    float m[NQ], l[NQ], o[NQ][VEC];
+#pragma unroll
+    for (int g = 0; g < NQ; ++g) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < R; ++r) mx = fmaxf(mx, s_log[slot * V + r * NQ + g]);
+      m[g] = mx;
+      l[g] = 0.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o[g][e] = 0.f;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = slot + NSLOT * r;
+      if (row < nrows) {
+        float vx[VEC];
+        E::unpack(vw[r], vx);
+#pragma unroll
+        for (int g = 0; g < NQ; ++g) {
+          const float pw = exp2f(s_log[slot * V + r * NQ + g] - m[g]);
+          l[g] += pw;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) o[g][e] = fmaf(pw, vx[e], o[g][e]);
+        }
+      }
+    }
+
+    // Merge the slots of this wave (lanes LPR apart) with shuffles.
+#pragma unroll
+    for (int b = LPR; b < kWave; b <<= 1) {
+#pragma unroll
+      for (int g = 0; g < NQ; ++g) {
+        const float m2 = __shfl_xor(m[g], b, kWave);
+        const float l2 = __shfl_xor(l[g], b, kWave);
+        const float mm = fmaxf(m[g], m2);
+        const float w1 = (m[g] == -INFINITY) ? 0.f : exp2f(m[g] - mm);
+        const float w2 = (m2 == -INFINITY) ? 0.f : exp2f(m2 - mm);
+        l[g] = l[g] * w1 + l2 * w2;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float o2 = __shfl_xor(o[g][e], b, kWave);
+          o[g][e] = o[g][e] * w1 + o2 * w2;
+        }
+        m[g] = mm;
+      }
+    }
+    if ((t & (kWave - 1)) < LPR) {
+#pragma unroll
+      for (int g = 0; g < NQ; ++g) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) s_o[(wave * NQ + g) * D + cc * VEC + e] = o[g][e];
+        if (cc == 0) { s_m[wave * NQ + g] = m[g]; s_l[wave * NQ + g] = l[g]; }
+      }
+    }
+    __syncthreads();
+
+    // Merge the waves and write the item's partial.
     float* po = p.part_o + (int64_t)item * kQG * D;
     float* pml = p.part_ml + (int64_t)item * kQG * 2;
     for (int e = t; e < NQ * D; e += blockDim.x) {
       const int g = e / D, d = e - g * D;
       float mm = -INFINITY;
 #pragma unroll
-      for (int s2 = 0; s2 < NSLOT; ++s2) mm = fmaxf(mm, s_m[s2 * NQ + g]);
+      for (int w = 0; w < NWAVE; ++w) mm = fmaxf(mm, s_m[w * NQ + g]);
       float acc = 0.f, ll = 0.f;
 #pragma unroll
-      for (int s2 = 0; s2 < NSLOT; ++s2) {
-        const float ms = s_m[s2 * NQ + g];
-        const float w = (ms == -INFINITY) ? 0.f : exp2f(ms - mm);
-        acc = fmaf(s_o[(s2 * NQ + g) * D + d], w, acc);
-        ll = fmaf(s_l[s2 * NQ + g], w, ll);
+      for (int w = 0; w < NWAVE; ++w) {
+        const float ms = s_m[w * NQ + g];
+        const float wt = (ms == -INFINITY) ? 0.f : exp2f(ms - mm);
+        acc = fmaf(s_o[(w * NQ + g) * D + d], wt, acc);
+        ll = fmaf(s_l[w * NQ + g], wt, ll);
       }
       po[g * D + d] = acc;
       if (d == 0) { pml[2 * g] = mm; pml[2 * g + 1] = ll; }
     }
     __syncthreads();
+    (void)SPW;
   }
 }
 
-// One workgroup per output row (segment, query token, query head): merge the
-// list's partials in item order, o / l, cast to the output dtype.  Zero rows
-// for an empty list.
+// Combine: one workgroup per (output row, 64-wide head_dim slice).  The four
+// waves split the list's items; weights exp2(m_i - M) and l go through LDS.
+constexpr int kCombineItems = 1024;  // items per LDS tile
+
 __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
   __shared__ int s_off[kMaxLists + 1];
+  __shared__ float s_w[kCombineItems];
+  __shared__ float s_red[16];
+  __shared__ float s_acc[4 * 64];
   const int nq_total = p.sq * p.group;
   const int nqg = (nq_total + kQG - 1) / kQG;
-  const int nlists = p.num_segments * p.num_kv_heads;
   build_item_offsets(p, s_off, nqg);
-  const int hq_count = p.num_kv_heads * p.group;
+  const int D = p.head_dim;
+  const int ndc = (D + 63) / 64;
   int id = blockIdx.x;
+  const int dc = id % ndc; id /= ndc;
+  const int hq_count = p.num_kv_heads * p.group;
   const int hq = id % hq_count; id /= hq_count;
   const int st = id % p.sq;
   const int seg = id / p.sq;
@@ -238,43 +349,75 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
   const int qi = st * p.group + g;
   const int qg = qi / kQG, ql = qi - qg * kQG;
   const int list = seg * p.num_kv_heads + h;
-  const int n = list_count(p, list) * p.nchunk;  // items of this query group
+  const int n = list_count(p, list) * p.nchunk;
   const int base = s_off[list];
-  const int D = p.head_dim;
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int wave = t / kWave;
+  const int d = dc * 64 + lane;
   const int64_t orow = (int64_t)seg * p.out_seg_stride + (int64_t)st * p.out_tok_stride +
                        (int64_t)hq * p.out_head_stride;
+
+  // Global max of m over the list's items.
   float mm = -INFINITY;
-  for (int j = 0; j < n; ++j) {
-    const int item = base + j * nqg + qg;
-    mm = fmaxf(mm, p.part_ml[((int64_t)item * kQG + ql) * 2]);
-  }
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float acc = 0.f, ll = 0.f;
-    for (int j = 0; j < n; ++j) {
-      const int item = base + j * nqg + qg;
-      const float mi = p.part_ml[((int64_t)item * kQG + ql) * 2];
+  for (int j = t; j < n; j += blockDim.x)
+    mm = fmaxf(mm, p.part_ml[((int64_t)(base + j * nqg + qg) * kQG + ql) * 2]);
+  mm = wave_max(mm);
+  if (lane == 0) s_red[wave] = mm;
+  __syncthreads();
+  mm = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  __syncthreads();
+
+  float acc = 0.f, ll = 0.f;
+  for (int j0 = 0; j0 < n; j0 += kCombineItems) {
+    const int jn = min(kCombineItems, n - j0);
+    for (int j = t; j < jn; j += blockDim.x) {
+      const int64_t it = (int64_t)(base + (j0 + j) * nqg + qg) * kQG + ql;
+      const float mi = p.part_ml[it * 2];
       const float w = (mi == -INFINITY) ? 0.f : exp2f(mi - mm);
-      acc = fmaf(p.part_o[((int64_t)item * kQG + ql) * D + d], w, acc);
-      ll = fmaf(p.part_ml[((int64_t)item * kQG + ql) * 2 + 1], w, ll);
+      s_w[j] = w;
+      ll = fmaf(p.part_ml[it * 2 + 1], w, ll);
     }
-    const float r = (n == 0) ? 0.f : acc / ll;
-    store_elt(p.out_dtype, p.out, orow + d, r);
+    __syncthreads();
+    if (d < D) {
+#pragma unroll 4
+      for (int j = wave; j < jn; j += 4) {
+        const int64_t it = (int64_t)(base + (j0 + j) * nqg + qg) * kQG + ql;
+        acc = fmaf(p.part_o[it * D + d], s_w[j], acc);
+      }
+    }
+    __syncthreads();
+  }
+  float lv[1] = {ll};
+  block_sum<1>(lv, s_red);
+  s_acc[wave * 64 + lane] = acc;
+  __syncthreads();
+  if (wave == 0 && d < D) {
+    const float a = s_acc[lane] + s_acc[64 + lane] + s_acc[128 + lane] + s_acc[192 + lane];
+    store_elt(p.out_dtype, p.out, orow + d, n == 0 ? 0.f : a / lv[0]);
   }
 }
 
 template <int DT, int LPR, int NQ>
 static hipError_t launch_attend_t(const AttendParams& p, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((attend_decode_kernel<DT, LPR, NQ>), dim3(grid), dim3(256), 0, s, p);
+  if (p.q_dtype == DT) {
+    hipLaunchKernelGGL((attend_decode_kernel<DT, LPR, NQ, DT>), dim3(grid), dim3(256), 0, s, p);
+  } else if (p.q_dtype == kF32) {
+    hipLaunchKernelGGL((attend_decode_kernel<DT, LPR, NQ, kF32>), dim3(grid), dim3(256), 0, s, p);
+  } else {
+    return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
 template <int DT, int LPR>
 static hipError_t launch_attend_nq(const AttendParams& p, int grid, hipStream_t s) {
-  const int nq = p.sq * p.group;
-  if (nq <= 1) return launch_attend_t<DT, LPR, 1>(p, grid, s);
-  if (nq <= 2) return launch_attend_t<DT, LPR, 2>(p, grid, s);
-  if (nq <= 4) return launch_attend_t<DT, LPR, 4>(p, grid, s);
-  return launch_attend_t<DT, LPR, 8>(p, grid, s);
+  switch (attend_nq_bucket(p.sq * p.group)) {
+    case 1: return launch_attend_t<DT, LPR, 1>(p, grid, s);
+    case 2: return launch_attend_t<DT, LPR, 2>(p, grid, s);
+    case 4: return launch_attend_t<DT, LPR, 4>(p, grid, s);
+    default: return launch_attend_t<DT, LPR, 8>(p, grid, s);
+  }
 }
 
 template <int DT>
@@ -286,6 +429,22 @@ static hipError_t launch_attend_dt(const AttendParams& p, int grid, hipStream_t 
     case 64: return launch_attend_nq<DT, 64>(p, grid, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+int attend_nq_bucket(int nq_total) {
+  if (nq_total <= 1) return 1;
+  if (nq_total <= 2) return 2;
+  if (nq_total <= 4) return 4;
+  return 8;
+}
+
+int attend_chunk(int dt, int head_dim, int nq_total) {
+  const int vec = (dt == kF32) ? 4 : 8;
+  const int lpr = head_dim / vec;
+  const int nslot = 256 / lpr;
+  const int nqb = attend_nq_bucket(nq_total);
+  const int r = nqb <= 2 ? rows_per_slot<2>() : (nqb == 4 ? rows_per_slot<4>() : rows_per_slot<8>());
+  return r * nslot;
 }
 
 bool attend_supported(int dt, int head_dim) {
@@ -317,7 +476,8 @@ hipError_t launch_attend(const AttendParams& p, hipStream_t s) {
   }
   const int rows = p.num_segments * p.sq * p.num_kv_heads * p.group;
   if (rows == 0) return hipSuccess;
-  hipLaunchKernelGGL(combine_kernel, dim3(rows), dim3(256), 0, s, p);
+  const int ndc = (p.head_dim + 63) / 64;
+  hipLaunchKernelGGL(combine_kernel, dim3(rows * ndc), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

@@ -102,7 +102,7 @@ struct CompactParams {
   int* num_active;         // (num_segments) or null
   int* head_indices;       // (Hkv, total_blocks) or null
   int* head_num_active;    // (num_segments, Hkv)
-  uint8_t* head_uniform;   // (num_segments, Hkv) or null
+  int* head_uniform;       // (num_segments, Hkv) or null
   int empty_head_all;
 };
 
@@ -122,7 +122,6 @@ hipError_t launch_copy_blocks(const CopyParams& p, hipStream_t s);
 // ---------------------------------------------------------- oc_attend.hip
 constexpr int kQG = 8;           // queries per attention work item
 constexpr int kMaxLists = 2048;  // (segments x kv heads) per launch
-constexpr int kChunk = 128;      // tokens per attention work item
 
 struct AttendParams {
   const void* q;
@@ -139,7 +138,7 @@ struct AttendParams {
   const int* indices;    // unified (total_blocks) or per head (Hkv, total_blocks)
   const int* counts;     // unified (num_segments) or per head (num_segments, Hkv)
   int per_head;
-  const uint8_t* uniform;  // (num_segments, Hkv) or null: equal weights on every token
+  const int* uniform;      // (num_segments, Hkv) or null: equal weights on every token
   float logit_scale;       // log2(e) / sqrt(head_dim)
   int chunk, nchunk;
   float* part_o;    // (max_items, kQG, D)
@@ -150,6 +149,8 @@ struct AttendParams {
 };
 
 bool attend_supported(int dt, int head_dim);
+int attend_nq_bucket(int nq_total);
+int attend_chunk(int dt, int head_dim, int nq_total);  // tokens per work item
 int64_t attend_max_items(const AttendParams& p);
 hipError_t launch_attend(const AttendParams& p, hipStream_t s);
 

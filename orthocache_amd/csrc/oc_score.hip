@@ -27,25 +27,18 @@
 
 namespace oc {
 
-__device__ __forceinline__ int find_segment(const int* cu, int nseg, int gb) {
-  if (cu == nullptr) return 0;
-  int lo = 0, hi = nseg - 1;
-  while (lo < hi) {
-    int mid = (lo + hi + 1) >> 1;
-    if (cu[mid] <= gb) lo = mid; else hi = mid - 1;
-  }
-  return lo;
-}
-
 template <int DT, int LPR>
 __device__ __forceinline__ void load_rows(const char* base, int64_t row_bytes, int l, uint4 (&r)[8]) {
 #pragma unroll
   for (int k = 0; k < 8; ++k) r[k] = ld16(base + (int64_t)(64 * k + l) * row_bytes);
 }
 
-template <int DT, int LPR>
+constexpr int kMaxSegLds = 4096;  // segments whose offsets are staged in LDS
+
+template <int DT, int LPR, int QDT>
 __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
   using E = Elt<DT>;
+  using EQ = Elt<QDT>;
   constexpr int VEC = E::VEC;
   constexpr int D = LPR * VEC;
   constexpr int NSLOT = 256 / LPR;
@@ -53,9 +46,11 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
   static_assert(NLO >= 2 && (NLO % 2) == 0, "unsupported lane layout");
   constexpr int ESZ = (DT == kF32) ? 4 : 2;
 
+  constexpr int NI = (D + 255) / 256;  // head_dim columns per thread in the epilogue
   __shared__ float s_mean[NSLOT * D];
   __shared__ float s_m2[NSLOT * D];
   __shared__ float s_red[64];
+  __shared__ int s_cu[kMaxSegLds + 1];
 
   const int tile = blockIdx.x;
   const int H = p.num_kv_heads;
@@ -69,6 +64,28 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
   const char* base = reinterpret_cast<const char*>(p.k) +
                      ((int64_t)gb * kBlock * p.k_tok_stride + (int64_t)h * p.k_head_stride +
                       (int64_t)cc * VEC) * ESZ;
+
+  // Query-aware bound inputs, requested before the key stream so their
+  // latency overlaps it: the segment table (ragged batches) goes to LDS, the
+  // first four queries' values of this thread's columns go to registers
+  // (one segment; a ragged batch needs the segment id first).
+  const bool want_bound = p.q != nullptr && p.tau_max != nullptr;
+  const int nq = p.sq * p.group;
+  if (want_bound && p.cu_blocks != nullptr) {
+    for (int i = t; i <= p.num_segments; i += 256) s_cu[i] = p.cu_blocks[i];
+  }
+  float qpre[4][NI];
+  const bool prefetch = want_bound && p.cu_blocks == nullptr && nq > 0;
+  if (prefetch) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int qi = min(u, nq - 1);
+      const int st = qi / p.group, g = qi - st * p.group;
+      const int64_t qoff = (int64_t)st * p.q_tok_stride + (int64_t)(h * p.group + g) * p.q_head_stride;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) qpre[u][i] = EQ::load1(p.q, qoff + min(t + 256 * i, D - 1));
+    }
+  }
 
   float acc_hi[VEC], acc_mid[VEC], piv[VEC], ssum[VEC], ssq[VEC];
 #pragma unroll
@@ -128,9 +145,9 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
 
   // Per column: merge the NSLOT partial (mean, M2) pairs (equal counts NLO).
   float elow = 0.f;
-  float kbar_r[(D + 255) / 256];
+  float kbar_r[NI];
 #pragma unroll
-  for (int i = 0; i < (D + 255) / 256; ++i) {
+  for (int i = 0; i < NI; ++i) {
     const int d = t + 256 * i;
     kbar_r[i] = 0.f;
     if (d < D) {
@@ -167,34 +184,51 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
 
   // Inline query-aware bound: tau_j = q.kbar/sqrt(d) + ||q|| sqrt(E_AC)/sqrt(d),
   // max over the segment's queries of every query head sharing kv head h.
-  if (p.q != nullptr && p.tau_max != nullptr) {
-    const int seg = find_segment(p.cu_blocks, p.num_segments, gb);
-    const int nq = p.sq * p.group;
+  if (want_bound) {
+    int seg = 0;
+    if (p.cu_blocks != nullptr) {
+      // s_cu was filled before the key stream; block_sum's barriers have
+      // made it visible.  Binary search for the segment holding block gb.
+      int lo = 0, hi = p.num_segments - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_cu[mid] <= gb) lo = mid; else hi = mid - 1;
+      }
+      seg = lo;
+    }
     const float sqrt_d = sqrtf((float)D);
     const float sqrt_eac = sqrtf(e_ac);
     float best = -INFINITY;
     for (int q0 = 0; q0 < nq; q0 += 4) {
-      float part[8];
+      float qv[4][NI];
+      if (prefetch && q0 == 0) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        part[2 * u] = 0.f;
-        part[2 * u + 1] = 0.f;
-        const int qi = q0 + u;
-        if (qi < nq) {
-          const int st = qi / p.group;
-          const int g = qi - st * p.group;
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int i = 0; i < NI; ++i) qv[u][i] = qpre[u][i];
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int qi = min(q0 + u, nq - 1);
+          const int st = qi / p.group, g = qi - st * p.group;
           const int64_t qoff = (int64_t)seg * p.q_seg_stride + (int64_t)st * p.q_tok_stride +
                                (int64_t)(h * p.group + g) * p.q_head_stride;
 #pragma unroll
-          for (int i = 0; i < (D + 255) / 256; ++i) {
-            const int d = t + 256 * i;
-            if (d < D) {
-              const float qv = load_elt(p.q_dtype, p.q, qoff + d);
-              part[2 * u] = fmaf(qv, kbar_r[i], part[2 * u]);
-              part[2 * u + 1] = fmaf(qv, qv, part[2 * u + 1]);
-            }
-          }
+          for (int i = 0; i < NI; ++i) qv[u][i] = EQ::load1(p.q, qoff + min(t + 256 * i, D - 1));
         }
+      }
+      float part[8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        float a = 0.f, b = 0.f;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          const float v = (t + 256 * i < D) ? qv[u][i] : 0.f;
+          a = fmaf(v, kbar_r[i], a);
+          b = fmaf(v, v, b);
+        }
+        part[2 * u] = a;
+        part[2 * u + 1] = b;
       }
       block_sum<8>(part, s_red);
 #pragma unroll
@@ -304,7 +338,15 @@ namespace oc {
 template <int DT, int LPR>
 static hipError_t launch_score_t(const ScoreParams& p, hipStream_t s) {
   const int tiles = p.total_blocks * p.num_kv_heads;
-  hipLaunchKernelGGL((score_kernel<DT, LPR>), dim3(tiles), dim3(256), 0, s, p);
+  // Without queries the query type is irrelevant: use the key type.
+  const int qdt = p.q ? p.q_dtype : DT;
+  if (qdt == DT) {
+    hipLaunchKernelGGL((score_kernel<DT, LPR, DT>), dim3(tiles), dim3(256), 0, s, p);
+  } else if (qdt == kF32) {
+    hipLaunchKernelGGL((score_kernel<DT, LPR, kF32>), dim3(tiles), dim3(256), 0, s, p);
+  } else {
+    return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
