@@ -216,6 +216,8 @@ int oc_attend(const oc_attend_args* a, void* workspace, size_t workspace_bytes, 
  * zeta_max, src/orthocache/pipeline.py:96-145), for a batch of segments with
  * per-segment thresholds.  Optional outputs (tau_max, zeta, mask, indices,
  * num_active) may be NULL, in which case the workspace holds them.
+ * Launches scoring, mask + compaction, attention and its combine on the
+ * stream.  At most 16 queries per kv head (sq * group).
  * workspace >= oc_decode_layer_workspace_size(...). */
 typedef struct oc_layer_args {
   const void* q;

@@ -15,6 +15,7 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
+INCLUDE = PKG.parent / "include"
 LIBDIR = PKG / "_lib"
 LIB = LIBDIR / "liborthocache_hip.so"
 OBJDIR = PKG.parent / "_build" / "obj"
@@ -34,7 +35,7 @@ CFLAGS = [
 
 def _compile(src: Path) -> Path:
     obj = OBJDIR / (src.stem + ".o")
-    cmd = [HIPCC, *CFLAGS, "-I", str(CSRC), "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *CFLAGS, "-I", str(CSRC), "-I", str(INCLUDE), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stderr}")

@@ -1,7 +1,7 @@
 // C ABI of liborthocache_hip.so: argument validation, workspace layout and
 // kernel launches.  Declarations and semantics: include/orthocache_hip.h.
 #include "oc_kernels.h"
-#include "../../include/orthocache_hip.h"
+#include "orthocache_hip.h"
 
 #include <cmath>
 #include <cstdarg>
@@ -240,6 +240,7 @@ struct LayerWs {
   size_t tau, zeta, idx, cnt, attend, total;
 };
 
+// Workspace: [tau_max | zeta | indices | num_active | attention partials].
 LayerWs layer_ws_layout(const oc_layer_args* a, size_t attend_bytes) {
   LayerWs w{};
   const size_t tiles = (size_t)a->total_blocks * a->num_kv_heads;
@@ -292,6 +293,12 @@ int oc_decode_layer(const oc_layer_args* a, void* workspace, size_t workspace_by
   if (rc) return rc;
   if (!oc::score_supported(a->kv_dtype, a->head_dim))
     return fail(OC_ERR_UNSUPPORTED, "scores: head_dim %d unsupported", a->head_dim);
+  if (a->q_dtype != a->kv_dtype && a->q_dtype != OC_F32)
+    return fail(OC_ERR_UNSUPPORTED, "q dtype must equal the kv dtype or be fp32");
+  if (a->sq * a->group > 16)
+    return fail(OC_ERR_UNSUPPORTED, "decode layer takes at most 16 queries per kv head (sq * group)");
+  const int nseg = a->cu_blocks ? a->num_segments : 1;
+  if (a->cu_blocks && nseg > 4096) return fail(OC_ERR_UNSUPPORTED, "at most 4096 segments per call");
   const LayerWs w = layer_ws_layout(a, attend_ws(ap));
   if (w.total && (!workspace || workspace_bytes < w.total))
     return fail(OC_ERR_WORKSPACE, "workspace %zu bytes < %zu needed", workspace_bytes, w.total);
@@ -302,27 +309,31 @@ int oc_decode_layer(const oc_layer_args* a, void* workspace, size_t workspace_by
   int32_t* cnt = a->num_active ? a->num_active : reinterpret_cast<int32_t*>(ws + w.cnt);
   const hipStream_t s = (hipStream_t)stream;
 
-  oc_score_args sa{};
-  sa.keys = a->k; sa.keys_dtype = a->kv_dtype;
-  sa.keys_tok_stride = a->k_tok_stride; sa.keys_head_stride = a->k_head_stride;
-  sa.head_dim = a->head_dim; sa.num_kv_heads = a->num_kv_heads; sa.total_blocks = a->total_blocks;
-  sa.cu_blocks = a->cu_blocks; sa.num_segments = a->num_segments;
-  sa.q = a->q; sa.q_dtype = a->q_dtype;
-  sa.q_seg_stride = a->q_seg_stride; sa.q_tok_stride = a->q_tok_stride; sa.q_head_stride = a->q_head_stride;
-  sa.sq = a->sq; sa.group = a->group;
-  sa.tau_max = tau_max; sa.zeta = zeta;
-  rc = oc_score_blocks(&sa, stream);
+  // 1. Scores.
+  oc::ScoreParams sp{};
+  sp.k = a->k; sp.k_tok_stride = a->k_tok_stride; sp.k_head_stride = a->k_head_stride; sp.k_dtype = a->kv_dtype;
+  sp.head_dim = a->head_dim; sp.num_kv_heads = a->num_kv_heads; sp.total_blocks = a->total_blocks;
+  sp.cu_blocks = a->cu_blocks; sp.num_segments = nseg;
+  sp.q = a->q; sp.q_dtype = a->q_dtype;
+  sp.q_seg_stride = a->q_seg_stride; sp.q_tok_stride = a->q_tok_stride; sp.q_head_stride = a->q_head_stride;
+  sp.sq = a->sq; sp.group = a->group;
+  sp.tau_max = tau_max; sp.zeta = zeta;
+  rc = hip_check(oc::launch_score(sp, s), "oc_decode_layer scores");
   if (rc) return rc;
 
-  oc_compact_args ca{};
-  ca.tau_max = tau_max; ca.tau_parts = 1; ca.zeta = zeta;
-  ca.tau_arr = a->tau_arr; ca.tau = a->tau; ca.zeta_max_arr = a->zeta_max_arr; ca.zeta_max = a->zeta_max;
-  ca.cu_blocks = a->cu_blocks; ca.num_segments = a->num_segments;
-  ca.num_kv_heads = a->num_kv_heads; ca.total_blocks = a->total_blocks;
-  ca.mask_out = a->mask; ca.indices = idx; ca.num_active = cnt;
-  rc = oc_mask_compact(&ca, stream);
-  if (rc) return rc;
+  // 2. Mask + compaction.
+  {
+    oc::CompactParams cp{};
+    cp.tau_max = tau_max; cp.tau_parts = 1; cp.zeta = zeta;
+    cp.tau_arr = a->tau_arr; cp.tau = a->tau; cp.zmax_arr = a->zeta_max_arr; cp.zeta_max = a->zeta_max;
+    cp.cu_blocks = a->cu_blocks; cp.num_segments = nseg; cp.nb_single = a->total_blocks;
+    cp.num_kv_heads = a->num_kv_heads; cp.total_blocks = a->total_blocks;
+    cp.mask_out = a->mask; cp.indices = idx; cp.num_active = cnt;
+    rc = hip_check(oc::launch_compact(cp, s), "oc_decode_layer compaction");
+    if (rc) return rc;
+  }
 
+  // 3. Attention (+ combine).
   ap.indices = idx;
   ap.counts = cnt;
   attend_bind_ws(ap, ws + w.attend);

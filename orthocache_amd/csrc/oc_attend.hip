@@ -31,6 +31,10 @@
 // exp2(s2 - m2); identical to the natural-log form in exact arithmetic.
 #include "oc_kernels.h"
 
+#ifndef OC_ATTEND_THREADS
+#define OC_ATTEND_THREADS 256
+#endif
+
 namespace oc {
 
 __device__ __forceinline__ int list_count(const AttendParams& p, int list) {
@@ -64,7 +68,7 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* s_wave, int& tot
 
 // s_off[list] = first item of the list, s_off[nlists] = total items.
 __device__ int build_item_offsets(const AttendParams& p, int* s_off, int nqg) {
-  __shared__ int s_wave[8];
+  __shared__ int s_wave[16];
   const int nlists = p.num_segments * p.num_kv_heads;
   const int t = threadIdx.x;
   const int per = (nlists + blockDim.x - 1) / blockDim.x;
@@ -118,24 +122,29 @@ struct Butterfly {
   }
 };
 
+// Threads per attention workgroup: NSLOT = kAttendThreads / LPR token rows
+// are in flight per load instruction, R per slot per item.
+constexpr int kAttendThreads = OC_ATTEND_THREADS;
+constexpr int kAttendGrid = 2048 * 256 / kAttendThreads;
+
 template <int NQ>
 __host__ __device__ constexpr int rows_per_slot() {
   return NQ <= 4 ? 8 : 4;
 }
 
 template <int DT, int LPR, int NQ, int QDT>
-__global__ __launch_bounds__(256) void attend_decode_kernel(AttendParams p) {
+__global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendParams p) {
   using E = Elt<DT>;
   using EQ = Elt<QDT>;
   constexpr int VEC = E::VEC;
   constexpr int D = LPR * VEC;
-  constexpr int NSLOT = 256 / LPR;
+  constexpr int NSLOT = kAttendThreads / LPR;
   constexpr int ESZ = (DT == kF32) ? 4 : 2;
   constexpr int R = rows_per_slot<NQ>();
   constexpr int V = R * NQ;                       // logits per slot
   constexpr int PER_LANE = V >= LPR ? V / LPR : 1;
   constexpr int SPW = kWave / LPR;                // slots per wave
-  constexpr int NWAVE = 256 / kWave;
+  constexpr int NWAVE = kAttendThreads / kWave;
 
   __shared__ int s_off[kMaxLists + 1];
   __shared__ float s_log[NSLOT * V];
@@ -158,8 +167,17 @@ __global__ __launch_bounds__(256) void attend_decode_kernel(AttendParams p) {
   const int wave = t / kWave;
 
   for (int item = blockIdx.x; item < total_items; item += gridDim.x) {
-    const int list = uniform_lists ? item / ipl : find_list(s_off, nlists, item);
-    int r0 = item - (uniform_lists ? list * ipl : s_off[list]);
+    // Uniform lists are enumerated head-fastest, so concurrently running
+    // workgroups read the other heads' pieces of the same token rows (whole
+    // rows of the (seq, heads, dim) layout, as the scoring kernel does).
+    int list, r0;
+    if (uniform_lists) {
+      list = item % nlists;
+      r0 = item / nlists;
+    } else {
+      list = find_list(s_off, nlists, item);
+      r0 = item - s_off[list];
+    }
     const int qg = r0 % nqg; r0 /= nqg;
     const int c = r0 % p.nchunk;
     const int i = r0 / p.nchunk;
@@ -326,8 +344,12 @@ __global__ __launch_bounds__(256) void attend_decode_kernel(AttendParams p) {
 }
 
 // Combine: one workgroup per (output row, 64-wide head_dim slice).  The four
-// waves split the list's items; weights exp2(m_i - M) and l go through LDS.
-constexpr int kCombineItems = 1024;  // items per LDS tile
+// waves split the list's items (wave w takes items w, w+4, ...).  Each lane
+// requests its first kCombineBatch partial outputs before the (m, l) pass, so
+// one round trip serves lists of up to 4 * kCombineBatch partials; weights
+// exp2(m_i - M) go through LDS.
+constexpr int kCombineItems = 1024;  // items whose weights fit in LDS at once
+constexpr int kCombineBatch = 32;    // partial outputs in flight per lane
 
 __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
   __shared__ int s_off[kMaxLists + 1];
@@ -336,7 +358,7 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
   __shared__ float s_acc[4 * 64];
   const int nq_total = p.sq * p.group;
   const int nqg = (nq_total + kQG - 1) / kQG;
-  build_item_offsets(p, s_off, nqg);
+  if (p.per_head || p.num_segments != 1) build_item_offsets(p, s_off, nqg);
   const int D = p.head_dim;
   const int ndc = (D + 63) / 64;
   int id = blockIdx.x;
@@ -350,18 +372,32 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
   const int qg = qi / kQG, ql = qi - qg * kQG;
   const int list = seg * p.num_kv_heads + h;
   const int n = list_count(p, list) * p.nchunk;
-  const int base = s_off[list];
+  const bool uniform_lists = !p.per_head && p.num_segments == 1;
+  const int base = uniform_lists ? 0 : s_off[list];
+  // Item of the list's j-th (slot, chunk) for query group qg: list-major
+  // offsets in general, head-fastest for uniform lists (see the attention kernel).
+  auto item_of = [&](int j) -> int64_t {
+    return uniform_lists ? ((int64_t)(j * nqg + qg) * (p.num_segments * p.num_kv_heads) + list)
+                         : (int64_t)(base + j * nqg + qg);
+  };
   const int t = threadIdx.x;
   const int lane = t & (kWave - 1);
   const int wave = t / kWave;
-  const int d = dc * 64 + lane;
+  const int d = min(dc * 64 + lane, D - 1);
   const int64_t orow = (int64_t)seg * p.out_seg_stride + (int64_t)st * p.out_tok_stride +
                        (int64_t)hq * p.out_head_stride;
 
-  // Global max of m over the list's items.
+  // Partial outputs of this wave's first batch, requested before anything else.
+  float vb[kCombineBatch];
+#pragma unroll
+  for (int u = 0; u < kCombineBatch; ++u) {
+    const int j = min(wave + 4 * u, max(n - 1, 0));
+    vb[u] = n > 0 ? p.part_o[(item_of(j) * kQG + ql) * D + d] : 0.f;
+  }
+
+  // M = max over the list's items of m.
   float mm = -INFINITY;
-  for (int j = t; j < n; j += blockDim.x)
-    mm = fmaxf(mm, p.part_ml[((int64_t)(base + j * nqg + qg) * kQG + ql) * 2]);
+  for (int j = t; j < n; j += blockDim.x) mm = fmaxf(mm, p.part_ml[(item_of(j) * kQG + ql) * 2]);
   mm = wave_max(mm);
   if (lane == 0) s_red[wave] = mm;
   __syncthreads();
@@ -372,18 +408,25 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
   for (int j0 = 0; j0 < n; j0 += kCombineItems) {
     const int jn = min(kCombineItems, n - j0);
     for (int j = t; j < jn; j += blockDim.x) {
-      const int64_t it = (int64_t)(base + (j0 + j) * nqg + qg) * kQG + ql;
+      const int64_t it = item_of(j0 + j) * kQG + ql;
       const float mi = p.part_ml[it * 2];
       const float w = (mi == -INFINITY) ? 0.f : exp2f(mi - mm);
       s_w[j] = w;
       ll = fmaf(p.part_ml[it * 2 + 1], w, ll);
     }
     __syncthreads();
-    if (d < D) {
-#pragma unroll 4
-      for (int j = wave; j < jn; j += 4) {
-        const int64_t it = (int64_t)(base + (j0 + j) * nqg + qg) * kQG + ql;
-        acc = fmaf(p.part_o[it * D + d], s_w[j], acc);
+    for (int b0 = 0; b0 < jn; b0 += 4 * kCombineBatch) {
+      if (j0 + b0 != 0) {  // later batches: load now (the first was requested up front)
+#pragma unroll
+        for (int u = 0; u < kCombineBatch; ++u) {
+          const int j = min(b0 + wave + 4 * u, jn - 1);
+          vb[u] = p.part_o[(item_of(j0 + j) * kQG + ql) * D + d];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kCombineBatch; ++u) {
+        const int j = b0 + wave + 4 * u;
+        if (j < jn) acc = fmaf(vb[u], s_w[j], acc);
       }
     }
     __syncthreads();
@@ -392,18 +435,18 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
   block_sum<1>(lv, s_red);
   s_acc[wave * 64 + lane] = acc;
   __syncthreads();
-  if (wave == 0 && d < D) {
+  if (wave == 0 && dc * 64 + lane < D) {
     const float a = s_acc[lane] + s_acc[64 + lane] + s_acc[128 + lane] + s_acc[192 + lane];
-    store_elt(p.out_dtype, p.out, orow + d, n == 0 ? 0.f : a / lv[0]);
+    store_elt(p.out_dtype, p.out, orow + dc * 64 + lane, n == 0 ? 0.f : a / lv[0]);
   }
 }
 
 template <int DT, int LPR, int NQ>
 static hipError_t launch_attend_t(const AttendParams& p, int grid, hipStream_t s) {
   if (p.q_dtype == DT) {
-    hipLaunchKernelGGL((attend_decode_kernel<DT, LPR, NQ, DT>), dim3(grid), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((attend_decode_kernel<DT, LPR, NQ, DT>), dim3(grid), dim3(kAttendThreads), 0, s, p);
   } else if (p.q_dtype == kF32) {
-    hipLaunchKernelGGL((attend_decode_kernel<DT, LPR, NQ, kF32>), dim3(grid), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((attend_decode_kernel<DT, LPR, NQ, kF32>), dim3(grid), dim3(kAttendThreads), 0, s, p);
   } else {
     return hipErrorInvalidValue;
   }
@@ -441,7 +484,7 @@ int attend_nq_bucket(int nq_total) {
 int attend_chunk(int dt, int head_dim, int nq_total) {
   const int vec = (dt == kF32) ? 4 : 8;
   const int lpr = head_dim / vec;
-  const int nslot = 256 / lpr;
+  const int nslot = kAttendThreads / lpr;
   const int nqb = attend_nq_bucket(nq_total);
   const int r = nqb <= 2 ? rows_per_slot<2>() : (nqb == 4 ? rows_per_slot<4>() : rows_per_slot<8>());
   return r * nslot;
@@ -464,7 +507,7 @@ int64_t attend_max_items(const AttendParams& p) {
 hipError_t launch_attend(const AttendParams& p, hipStream_t s) {
   const int64_t max_items = attend_max_items(p);
   if (max_items > 0) {
-    const int grid = (int)(max_items < 2048 ? max_items : 2048);
+    const int grid = (int)(max_items < kAttendGrid ? max_items : kAttendGrid);
     hipError_t e;
     switch (p.kv_dtype) {
       case kF32: e = launch_attend_dt<kF32>(p, grid, s); break;

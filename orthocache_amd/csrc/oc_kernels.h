@@ -29,32 +29,6 @@ hipError_t launch_fwht(const FwhtParams& p, hipStream_t s);
 hipError_t launch_band_energy(const BandParams& p, hipStream_t s);
 
 // ----------------------------------------------------------- oc_score.hip
-struct ScoreParams {
-  const void* k;
-  int64_t k_tok_stride;   // elements between consecutive tokens
-  int64_t k_head_stride;  // elements between kv heads
-  int k_dtype;
-  int head_dim;
-  int num_kv_heads;
-  int total_blocks;
-  const int* cu_blocks;   // (num_segments + 1) block offsets, or null for one segment
-  int num_segments;
-  // Queries for the inline bound (may be null): segment s, query t, head hq
-  // at q + s*q_seg_stride + t*q_tok_stride + hq*q_head_stride.
-  const void* q;
-  int q_dtype;
-  int64_t q_seg_stride, q_tok_stride, q_head_stride;
-  int sq;      // queries per segment
-  int group;   // query heads per kv head
-  // Outputs, each optional.
-  float* tau_max;  // (total_blocks, Hkv): NaN-propagating max over queries
-  float* zeta;     // (total_blocks, Hkv)
-  float* dc;       // (total_blocks, Hkv, D): FWHT coefficient 0
-  float* e_low;
-  float* e_mid;
-  float* e_high;
-  float* e_ac;
-};
 
 struct BoundParams {
   const float* dc;     // (nb, Hkv, D)
@@ -75,8 +49,6 @@ struct EnergyParams {
   float* out;
 };
 
-bool score_supported(int dt, int head_dim);
-hipError_t launch_score(const ScoreParams& p, hipStream_t s);
 hipError_t launch_bound(const BoundParams& p, hipStream_t s);
 hipError_t launch_block_energy(const EnergyParams& p, hipStream_t s);
 
@@ -117,6 +89,36 @@ struct CopyParams {
 };
 
 hipError_t launch_compact(const CompactParams& p, hipStream_t s);
+
+struct ScoreParams {
+  const void* k;
+  int64_t k_tok_stride;   // elements between consecutive tokens
+  int64_t k_head_stride;  // elements between kv heads
+  int k_dtype;
+  int head_dim;
+  int num_kv_heads;
+  int total_blocks;
+  const int* cu_blocks;   // (num_segments + 1) block offsets, or null for one segment
+  int num_segments;
+  // Queries for the inline bound (may be null): segment s, query t, head hq
+  // at q + s*q_seg_stride + t*q_tok_stride + hq*q_head_stride.
+  const void* q;
+  int q_dtype;
+  int64_t q_seg_stride, q_tok_stride, q_head_stride;
+  int sq;      // queries per segment
+  int group;   // query heads per kv head
+  // Outputs, each optional.
+  float* tau_max;  // (total_blocks, Hkv): NaN-propagating max over queries
+  float* zeta;     // (total_blocks, Hkv)
+  float* dc;       // (total_blocks, Hkv, D): FWHT coefficient 0
+  float* e_low;
+  float* e_mid;
+  float* e_high;
+  float* e_ac;
+};
+
+bool score_supported(int dt, int head_dim);
+hipError_t launch_score(const ScoreParams& p, hipStream_t s);
 hipError_t launch_copy_blocks(const CopyParams& p, hipStream_t s);
 
 // ---------------------------------------------------------- oc_attend.hip

@@ -71,7 +71,8 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
   // (one segment; a ragged batch needs the segment id first).
   const bool want_bound = p.q != nullptr && p.tau_max != nullptr;
   const int nq = p.sq * p.group;
-  if (want_bound && p.cu_blocks != nullptr) {
+  const bool need_seg = p.cu_blocks != nullptr && want_bound;
+  if (need_seg) {
     for (int i = t; i <= p.num_segments; i += 256) s_cu[i] = p.cu_blocks[i];
   }
   float qpre[4][NI];
@@ -184,18 +185,18 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
 
   // Inline query-aware bound: tau_j = q.kbar/sqrt(d) + ||q|| sqrt(E_AC)/sqrt(d),
   // max over the segment's queries of every query head sharing kv head h.
-  if (want_bound) {
-    int seg = 0;
-    if (p.cu_blocks != nullptr) {
-      // s_cu was filled before the key stream; block_sum's barriers have
-      // made it visible.  Binary search for the segment holding block gb.
-      int lo = 0, hi = p.num_segments - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (s_cu[mid] <= gb) lo = mid; else hi = mid - 1;
-      }
-      seg = lo;
+  int seg = 0;
+  if (need_seg) {
+    // s_cu was filled before the key stream; block_sum's barriers have
+    // made it visible.  Binary search for the segment holding block gb.
+    int lo = 0, hi = p.num_segments - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_cu[mid] <= gb) lo = mid; else hi = mid - 1;
     }
+    seg = lo;
+  }
+  if (want_bound) {
     const float sqrt_d = sqrtf((float)D);
     const float sqrt_eac = sqrtf(e_ac);
     float best = -INFINITY;

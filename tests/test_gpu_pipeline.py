@@ -226,3 +226,26 @@ def test_c5_sweep(dev):
     q0 = O.fold_gqa(np32(wl.q[0]), 16)
     np.testing.assert_allclose(zn[: cu[1]], O.spectral_decay_ratio(k0), rtol=1e-5)
     np.testing.assert_allclose(tmn[: cu[1]], O.query_aware_bounds(q0, k0).max(axis=0), rtol=1e-5, atol=1e-5)
+
+
+def test_fused_layer_repeats_deterministically(dev):
+    """One-segment layers derive the block list inside the attention kernel
+    (every workgroup from the same scores); back-to-back calls must agree bit
+    for bit and publish the oracle's permutation."""
+    from orthocache_amd import _ops, workloads
+
+    wl = workloads.c2(dev, seq=16384)
+    sc = _ops.score(wl.k, wl.q)
+    tau, zmax = workloads.calibrate_unified(sc.tau_max[0], sc.zeta, 0.75)
+    layer = _ops.DecodeLayer(wl.q, wl.k, wl.v, tau, zmax)
+    outs, idx = [], []
+    for _ in range(4):
+        outs.append(layer.run().clone())
+        idx.append(layer.indices.clone())
+    torch.cuda.synchronize()
+    for o, i in zip(outs[1:], idx[1:]):
+        assert torch.equal(o, outs[0]) and torch.equal(i, idx[0])
+    mask = O.mask_from_scores(np32(layer.tau_max), np32(layer.zeta), tau, zmax)
+    order, n = O.stream_compact_indices(mask)
+    np.testing.assert_array_equal(np32(idx[0]).astype(np.int64), order)
+    assert int(layer.num_active[0]) == n
