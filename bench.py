@@ -40,6 +40,8 @@ def parse():
     p.add_argument("--kernel-reps", type=int, default=100)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
+    p.add_argument("--copy-probe-mib", type=int, default=0,
+                   help="first run a plain device copy of this many MiB (reference for HBM counters)")
     return p.parse_args()
 
 
@@ -130,6 +132,15 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     print(f"bench: lib {_native.LIB_PATH}", file=sys.stderr, flush=True)
+
+    if args.copy_probe_mib:
+        n = args.copy_probe_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     wl = workloads.c2(dev, seq=args.seq)
     sc = _ops.score(wl.k, wl.q)
