@@ -199,9 +199,9 @@ __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendPar
     // branch) and rows past nrows are masked afterwards.
     uint4 kw[R], vw[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) kw[r] = ld16(kb + min(slot + NSLOT * r, nrows - 1) * krow);
+    for (int r = 0; r < R; ++r) kw[r] = ld16_nt(kb + min(slot + NSLOT * r, nrows - 1) * krow);
 #pragma unroll
-    for (int r = 0; r < R; ++r) vw[r] = ld16(vb + min(slot + NSLOT * r, nrows - 1) * vrow);
+    for (int r = 0; r < R; ++r) vw[r] = ld16_nt(vb + min(slot + NSLOT * r, nrows - 1) * vrow);
 
     // Queries (pre-scaled by log2(e)/sqrt(d)); 16-byte loads of the lane's
     // VEC elements, query index clamped and missing queries zeroed.

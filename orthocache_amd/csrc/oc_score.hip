@@ -30,7 +30,7 @@ namespace oc {
 template <int DT, int LPR>
 __device__ __forceinline__ void load_rows(const char* base, int64_t row_bytes, int l, uint4 (&r)[8]) {
 #pragma unroll
-  for (int k = 0; k < 8; ++k) r[k] = ld16(base + (int64_t)(64 * k + l) * row_bytes);
+  for (int k = 0; k < 8; ++k) r[k] = ld16_nt(base + (int64_t)(64 * k + l) * row_bytes);
 }
 
 constexpr int kMaxSegLds = 4096;  // segments whose offsets are staged in LDS
