@@ -194,17 +194,10 @@ __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendPar
                      (tok0 * p.v_tok_stride + (int64_t)h * p.v_head_stride + (int64_t)cc * VEC) * ESZ;
     const int64_t krow = p.k_tok_stride * ESZ, vrow = p.v_tok_stride * ESZ;
 
-    // Issue every K and V load of this item first.  Row indices are clamped
-    // into the block (loads stay unconditional, so none waits behind a
-    // branch) and rows past nrows are masked afterwards.
-    uint4 kw[R], vw[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) kw[r] = ld16_nt(kb + min(slot + NSLOT * r, nrows - 1) * krow);
-#pragma unroll
-    for (int r = 0; r < R; ++r) vw[r] = ld16_nt(vb + min(slot + NSLOT * r, nrows - 1) * vrow);
-
     // Queries (pre-scaled by log2(e)/sqrt(d)); 16-byte loads of the lane's
-    // VEC elements, query index clamped and missing queries zeroed.
+    // VEC elements, query index clamped and missing queries zeroed.  They are
+    // requested before K and V: loads retire in order, so the dot products
+    // then wait only for K while V is still arriving.
     float qv[NQ][VEC];
 #pragma unroll
     for (int g = 0; g < NQ; ++g) {
@@ -224,6 +217,15 @@ __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendPar
         for (int e = 0; e < EQ::VEC && e0 + e < VEC; ++e) qv[g][e0 + e] = tmp[e] * sc;
       }
     }
+
+    // Every K and V load of the item, before any arithmetic.  Row indices are clamped
+    // into the block (loads stay unconditional, so none waits behind a
+    // branch) and rows past nrows are masked afterwards.
+    uint4 kw[R], vw[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) kw[r] = ld16_nt(kb + min(slot + NSLOT * r, nrows - 1) * krow);
+#pragma unroll
+    for (int r = 0; r < R; ++r) vw[r] = ld16_nt(vb + min(slot + NSLOT * r, nrows - 1) * vrow);
 
     // Uniform per workgroup: a scalar load, which does not wait on the K/V loads.
     const bool uni = (p.uniform != nullptr) && (p.uniform[list] != 0);
@@ -343,18 +345,19 @@ __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendPar
   }
 }
 
-// Combine: one workgroup per (output row, 64-wide head_dim slice).  The four
-// waves split the list's items (wave w takes items w, w+4, ...).  Each lane
-// requests its first kCombineBatch partial outputs before the (m, l) pass, so
-// one round trip serves lists of up to 4 * kCombineBatch partials; weights
-// exp2(m_i - M) go through LDS.
-constexpr int kCombineItems = 1024;  // items whose weights fit in LDS at once
-constexpr int kCombineBatch = 32;    // partial outputs in flight per lane
+// Combine: one workgroup per (output row, 64-wide head_dim slice).  Wave w
+// takes the list's items w, w+4, ... in rounds of kCombineBatch items: each
+// lane requests the partial outputs of the round's items for its column and
+// lane u the (m, l) of item u, all before any arithmetic, so one round trip
+// serves a round (lists of up to 4 * kCombineBatch partials take one).
+// Within a wave the rounds merge online (running max, rescaled sums); the
+// four waves merge through LDS.  The order is fixed, so the result is
+// deterministic.
+constexpr int kCombineBatch = 32;  // items per wave per round (lanes 0..31 hold their m, l)
 
 __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
   __shared__ int s_off[kMaxLists + 1];
-  __shared__ float s_w[kCombineItems];
-  __shared__ float s_red[16];
+  __shared__ float s_ml[2 * 4];
   __shared__ float s_acc[4 * 64];
   const int nq_total = p.sq * p.group;
   const int nqg = (nq_total + kQG - 1) / kQG;
@@ -375,69 +378,62 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
   const bool uniform_lists = !p.per_head && p.num_segments == 1;
   const int base = uniform_lists ? 0 : s_off[list];
   // Item of the list's j-th (slot, chunk) for query group qg: list-major
-  // offsets in general, head-fastest for uniform lists (see the attention kernel).
+  // offsets in general, head-fastest for uniform lists (as the attention
+  // kernel enumerates them).
   auto item_of = [&](int j) -> int64_t {
     return uniform_lists ? ((int64_t)(j * nqg + qg) * (p.num_segments * p.num_kv_heads) + list)
                          : (int64_t)(base + j * nqg + qg);
   };
   const int t = threadIdx.x;
   const int lane = t & (kWave - 1);
-  const int wave = t / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
   const int d = min(dc * 64 + lane, D - 1);
   const int64_t orow = (int64_t)seg * p.out_seg_stride + (int64_t)st * p.out_tok_stride +
                        (int64_t)hq * p.out_head_stride;
 
-  // Partial outputs of this wave's first batch, requested before anything else.
-  float vb[kCombineBatch];
+  float m_run = -INFINITY, l_run = 0.f, acc = 0.f;
+  const int last = max(n - 1, 0);
+  for (int b0 = 0; b0 < n; b0 += 4 * kCombineBatch) {
+    // Requests first: partial outputs (clamped indices) and lane u's (m, l).
+    float ov[kCombineBatch];
 #pragma unroll
-  for (int u = 0; u < kCombineBatch; ++u) {
-    const int j = min(wave + 4 * u, max(n - 1, 0));
-    vb[u] = n > 0 ? p.part_o[(item_of(j) * kQG + ql) * D + d] : 0.f;
-  }
-
-  // M = max over the list's items of m.
-  float mm = -INFINITY;
-  for (int j = t; j < n; j += blockDim.x) mm = fmaxf(mm, p.part_ml[(item_of(j) * kQG + ql) * 2]);
-  mm = wave_max(mm);
-  if (lane == 0) s_red[wave] = mm;
-  __syncthreads();
-  mm = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-  __syncthreads();
-
-  float acc = 0.f, ll = 0.f;
-  for (int j0 = 0; j0 < n; j0 += kCombineItems) {
-    const int jn = min(kCombineItems, n - j0);
-    for (int j = t; j < jn; j += blockDim.x) {
-      const int64_t it = item_of(j0 + j) * kQG + ql;
-      const float mi = p.part_ml[it * 2];
-      const float w = (mi == -INFINITY) ? 0.f : exp2f(mi - mm);
-      s_w[j] = w;
-      ll = fmaf(p.part_ml[it * 2 + 1], w, ll);
+    for (int u = 0; u < kCombineBatch; ++u) {
+      const int j = min(b0 + wave + 4 * u, last);
+      ov[u] = p.part_o[(item_of(j) * kQG + ql) * D + d];
     }
-    __syncthreads();
-    for (int b0 = 0; b0 < jn; b0 += 4 * kCombineBatch) {
-      if (j0 + b0 != 0) {  // later batches: load now (the first was requested up front)
+    const int ju = b0 + wave + 4 * (lane % kCombineBatch);
+    const float2 ml = *reinterpret_cast<const float2*>(p.part_ml + (item_of(min(ju, last)) * kQG + ql) * 2);
+    const bool valid = lane < kCombineBatch && ju < n;
+    const float mi = valid ? ml.x : -INFINITY;
+
+    const float m_new = fmaxf(m_run, wave_max(mi));
+    const float scale = (m_run == -INFINITY) ? 0.f : exp2f(m_run - m_new);
+    const float w = (mi == -INFINITY) ? 0.f : exp2f(mi - m_new);
+    l_run = l_run * scale + wave_sum(valid ? w * ml.y : 0.f);
+    acc *= scale;
 #pragma unroll
-        for (int u = 0; u < kCombineBatch; ++u) {
-          const int j = min(b0 + wave + 4 * u, jn - 1);
-          vb[u] = p.part_o[(item_of(j0 + j) * kQG + ql) * D + d];
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < kCombineBatch; ++u) {
-        const int j = b0 + wave + 4 * u;
-        if (j < jn) acc = fmaf(vb[u], s_w[j], acc);
-      }
+    for (int u = 0; u < kCombineBatch; ++u) {
+      const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
+      if (b0 + wave + 4 * u < n) acc = fmaf(wu, ov[u], acc);
     }
-    __syncthreads();
+    m_run = m_new;
   }
-  float lv[1] = {ll};
-  block_sum<1>(lv, s_red);
+  if (lane == 0) { s_ml[2 * wave] = m_run; s_ml[2 * wave + 1] = l_run; }
   s_acc[wave * 64 + lane] = acc;
   __syncthreads();
   if (wave == 0 && dc * 64 + lane < D) {
-    const float a = s_acc[lane] + s_acc[64 + lane] + s_acc[128 + lane] + s_acc[192 + lane];
-    store_elt(p.out_dtype, p.out, orow + dc * 64 + lane, n == 0 ? 0.f : a / lv[0]);
+    float mm = -INFINITY;
+#pragma unroll
+    for (int w2 = 0; w2 < 4; ++w2) mm = fmaxf(mm, s_ml[2 * w2]);
+    float a = 0.f, ll = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < 4; ++w2) {
+      const float mw = s_ml[2 * w2];
+      const float sw = (mw == -INFINITY) ? 0.f : exp2f(mw - mm);
+      a = fmaf(s_acc[w2 * 64 + lane], sw, a);
+      ll = fmaf(s_ml[2 * w2 + 1], sw, ll);
+    }
+    store_elt(p.out_dtype, p.out, orow + dc * 64 + lane, n == 0 ? 0.f : a / ll);
   }
 }
 

@@ -12,6 +12,8 @@
 //   E_high = 1/2 * sum_l sum_{k<4} (x_k - x_{k+4})^2            (index bit 8 set)
 //   u_k    = x_k + x_{k+4},  y = WHT4(u)
 //   E_mid  = 1/8 * sum_l (y1^2 + y2^2 + y3^2)                    (bits 6/7 set, 8 clear)
+//          = 1/8 * sum_l (2 a1^2 + 2 a3^2 + y2^2), with a1 = u0 - u1, a3 = u2 - u3,
+//            since y1^2 + y3^2 = (a1 + a3)^2 + (a1 - a3)^2
 //   E_low  = 1/8 * sum_l (y0_l - mean_l y0)^2                    (coset 0 minus DC)
 //   DC     = sum_l y0_l / sqrt(512),  kbar = DC / sqrt(512)
 // so one pass over the keys, ~4 VALU ops per element, gives every score the
@@ -88,9 +90,9 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
     }
   }
 
-  float acc_hi[VEC], acc_mid[VEC], piv[VEC], ssum[VEC], ssq[VEC];
+  float acc_hi[VEC], acc_mid[VEC], acc_mid2[VEC], piv[VEC], ssum[VEC], ssq[VEC];
 #pragma unroll
-  for (int c = 0; c < VEC; ++c) { acc_hi[c] = 0.f; acc_mid[c] = 0.f; ssum[c] = 0.f; ssq[c] = 0.f; piv[c] = 0.f; }
+  for (int c = 0; c < VEC; ++c) { acc_hi[c] = 0.f; acc_mid[c] = 0.f; acc_mid2[c] = 0.f; ssum[c] = 0.f; ssq[c] = 0.f; piv[c] = 0.f; }
 
   auto consume = [&](const uint4 (&r)[8], bool first) {
     float x[8][VEC];
@@ -106,10 +108,10 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
       const float u0 = x[0][c] + x[4][c], u1 = x[1][c] + x[5][c];
       const float u2 = x[2][c] + x[6][c], u3 = x[3][c] + x[7][c];
       const float a0 = u0 + u1, a1 = u0 - u1, a2 = u2 + u3, a3 = u2 - u3;
-      const float y0 = a0 + a2, y1 = a1 + a3, y2 = a0 - a2, y3 = a1 - a3;
-      float am = acc_mid[c];
-      am = fmaf(y1, y1, am); am = fmaf(y2, y2, am); am = fmaf(y3, y3, am);
-      acc_mid[c] = am;
+      const float y0 = a0 + a2, y2 = a0 - a2;
+      float am = acc_mid[c], am2 = acc_mid2[c];
+      am2 = fmaf(a1, a1, am2); am2 = fmaf(a3, a3, am2); am = fmaf(y2, y2, am);
+      acc_mid[c] = am; acc_mid2[c] = am2;
       if (first) {
         piv[c] = y0;
       } else {
@@ -134,7 +136,7 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
 #pragma unroll
   for (int c = 0; c < VEC; ++c) {
     hi += acc_hi[c];
-    mid += acc_mid[c];
+    mid += acc_mid[c] + 2.f * acc_mid2[c];
     const float mean_t = piv[c] + ssum[c] * (1.f / NLO);
     // Clamp rounding below zero without dropping NaN (fmaxf would).
     const float m2_raw = ssq[c] - ssum[c] * ssum[c] * (1.f / NLO);

@@ -109,8 +109,9 @@ def _kernel_band_identity(block):
     e_high = 0.5 * np.sum(d * d)
     u = x[:4] + x[4:]
     a0, a1, a2, a3 = u[0] + u[1], u[0] - u[1], u[2] + u[3], u[2] - u[3]
-    y0, y1, y2, y3 = a0 + a2, a1 + a3, a0 - a2, a1 - a3
-    e_mid = 0.125 * np.sum(y1 * y1 + y2 * y2 + y3 * y3)
+    # The kernel forms y1^2 + y3^2 as 2 a1^2 + 2 a3^2 (y1, y3 = a1 +- a3).
+    y0, y2 = a0 + a2, a0 - a2
+    e_mid = 0.125 * np.sum(2.0 * a1 * a1 + 2.0 * a3 * a3 + y2 * y2)
     e_low = 0.125 * np.sum((y0 - y0.mean(axis=0, keepdims=True)) ** 2)
     dc = y0.sum(axis=0) / np.sqrt(512)
     return dc, e_low, e_mid, e_high
