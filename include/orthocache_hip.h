@@ -184,9 +184,14 @@ int oc_copy_blocks(const void* src, void* dst, const int32_t* indices, const int
  * (src/orthocache/adaptive_attention.py:46-184), indirect_attention
  * (src/orthocache/indirect_attention.py:127-170) and the kernel of
  * compile_pallas_sparse_attention (src/orthocache/sparse_attention.py:67-180).
- * Decode form: any sq*group (work is split in groups of 8 queries; large
- * query counts re-read K/V once per group).  head_dim/(16/esize) in
- * {8,16,32,64}.  workspace >= oc_attend_workspace_size(...). */
+ * Two kernel families, chosen per call (oc_attend_plan reports which):
+ *  - decode: any sq*group (work split in groups of 8 queries; large query
+ *    counts re-read K/V once per group); head_dim/(16/esize) in {8,16,32,64};
+ *  - prefill (matrix cores): bf16 or fp16 q, K and V of one dtype,
+ *    head_dim 64 or 128, block_size a multiple of 64 and at least 32 query
+ *    rows (sq * group) per kv head; Q K^T and P V on bf16/fp16 MFMA tiles with
+ *    fp32 softmax state, P rounded to the input dtype for the P V product.
+ * workspace >= oc_attend_workspace_size(...). */
 typedef struct oc_attend_args {
   const void* q;
   int32_t q_dtype;
@@ -209,6 +214,15 @@ typedef struct oc_attend_args {
 } oc_attend_args;
 size_t oc_attend_workspace_size(const oc_attend_args* a);
 int oc_attend(const oc_attend_args* a, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Which kernel family oc_attend uses for these arguments, and for the prefill
+ * kernels the number of ways each list's tile range is split.  No
+ * counterpart in the reference (its dispatch is the Python-side `path`
+ * label of adaptive_attention.py:172-183); it lets callers and tests check
+ * the choice without a device. */
+#define OC_ATTEND_DECODE 0
+#define OC_ATTEND_PREFILL_MFMA 1
+int oc_attend_plan(const oc_attend_args* a, int32_t* kernel, int32_t* nsplit);
 
 /* ---------------------------------------------------------------- one layer
  * The hot path in one call: oc_score_blocks -> oc_mask_compact -> oc_attend

@@ -90,7 +90,7 @@ class LayerArgs(C.Structure):
 EXPORTED_SYMBOLS = (
     "oc_last_error", "oc_abi_version", "oc_fwht512", "oc_band_energy", "oc_block_energy",
     "oc_score_blocks", "oc_query_bounds", "oc_query_bound_tiles", "oc_mask_compact",
-    "oc_copy_blocks", "oc_attend_workspace_size", "oc_attend",
+    "oc_copy_blocks", "oc_attend_workspace_size", "oc_attend", "oc_attend_plan",
     "oc_decode_layer_workspace_size", "oc_decode_layer",
 )
 
@@ -118,6 +118,7 @@ def lib() -> C.CDLL:
         ("oc_mask_compact", [C.POINTER(CompactArgs), _vp]),
         ("oc_copy_blocks", [_vp, _vp, _vp, _vp, _i32, _i64, _i32, _vp]),
         ("oc_attend", [C.POINTER(AttendArgs), _vp, C.c_size_t, _vp]),
+        ("oc_attend_plan", [C.POINTER(AttendArgs), C.POINTER(_i32), C.POINTER(_i32)]),
         ("oc_decode_layer", [C.POINTER(LayerArgs), _vp, C.c_size_t, _vp]),
     ):
         f = getattr(L, name)

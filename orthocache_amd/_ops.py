@@ -272,6 +272,30 @@ def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, indices: torch.Ten
            num_segments: int = 1, out: torch.Tensor | None = None) -> torch.Tensor:
     """Attention over the listed blocks.  q: (Sq, Hq, D) (or (B, Sq, Hq, D) with
     cu_blocks); k, v: (S, Hkv, D).  Returns q-shaped output in out_dtype."""
+    a, out, q = _attend_args(q, k, v, indices, counts, block_size=block_size, per_head=per_head, uniform=uniform,
+                             out_dtype=out_dtype, cu_blocks=cu_blocks, num_segments=num_segments, out=out)
+    L = lib()
+    ws_bytes = int(L.oc_attend_workspace_size(C.byref(a)))
+    if ws_bytes == 0 and a.total_blocks > 0:
+        # Size query failed validation: surface the message.
+        check(L.oc_attend(C.byref(a), None, 0, stream_ptr(q.device)), "oc_attend")
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=q.device)
+    check(L.oc_attend(C.byref(a), ptr(ws), ws_bytes, stream_ptr(q.device)), "oc_attend")
+    return out
+
+
+def attend_plan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, indices: torch.Tensor, counts: torch.Tensor,
+                **kw) -> tuple[str, int]:
+    """Kernel family ``attend`` would use for these arguments ("decode" or
+    "prefill_mfma") and the prefill split count (0 for decode)."""
+    a, _, _ = _attend_args(q, k, v, indices, counts, **kw)
+    kern, nsplit = C.c_int32(), C.c_int32()
+    check(lib().oc_attend_plan(C.byref(a), C.byref(kern), C.byref(nsplit)), "oc_attend_plan")
+    return ("prefill_mfma" if kern.value == 1 else "decode"), int(nsplit.value)
+
+
+def _attend_args(q, k, v, indices, counts, *, block_size: int = BLOCK, per_head: bool = False,
+                 uniform=None, out_dtype=None, cu_blocks=None, num_segments: int = 1, out=None):
     require_gpu(q, k, v, indices, counts)
     out_dtype = out_dtype or q.dtype
     k = _kv_view(k, "keys")
@@ -305,14 +329,7 @@ def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, indices: torch.Ten
     a.out = ptr(out); a.out_dtype = dtype_code(out.dtype)
     a.out_seg_stride = out.stride(0) if out.dim() == 4 else 0
     a.out_tok_stride = out.stride(-3); a.out_head_stride = out.stride(-2)
-    L = lib()
-    ws_bytes = int(L.oc_attend_workspace_size(C.byref(a)))
-    if ws_bytes == 0 and a.total_blocks > 0:
-        # Size query failed validation: surface the message.
-        check(L.oc_attend(C.byref(a), None, 0, stream_ptr(q.device)), "oc_attend")
-    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=q.device)
-    check(L.oc_attend(C.byref(a), ptr(ws), ws_bytes, stream_ptr(q.device)), "oc_attend")
-    return out
+    return a, out, q
 
 
 # ------------------------------------------------------------- one layer

@@ -194,20 +194,30 @@ int make_attend_params(const oc_attend_args* a, oc::AttendParams& p) {
   p.part_o = nullptr; p.part_ml = nullptr;
   p.out = a->out; p.out_dtype = a->out_dtype;
   p.out_seg_stride = a->out_seg_stride; p.out_tok_stride = a->out_tok_stride; p.out_head_stride = a->out_head_stride;
+  p.prefill = oc::prefill_supported(a->kv_dtype, a->q_dtype, a->head_dim, a->sq * a->group, a->block_size) ? 1 : 0;
+  // The prefill kernel keeps per-thread offsets inside a 64-token tile in 32 bits.
+  if (a->k_tok_stride >= (1 << 24) || a->v_tok_stride >= (1 << 24)) p.prefill = 0;
+  p.nsplit = p.prefill ? oc::prefill_nsplit(p) : 0;
   return OC_OK;
 }
 
-size_t attend_ws(const oc::AttendParams& p) {
-  const int64_t items = oc::attend_max_items(p);
-  return align256((size_t)items * oc::kQG * p.head_dim * sizeof(float)) +
-         align256((size_t)items * oc::kQG * 2 * sizeof(float));
+// Partial-result bytes: [o | (m, l)].
+size_t attend_part_o_bytes(const oc::AttendParams& p) {
+  if (p.prefill) return align256((size_t)oc::prefill_partial_floats(p) * sizeof(float));
+  return align256((size_t)oc::attend_max_items(p) * oc::kQG * p.head_dim * sizeof(float));
 }
 
+size_t attend_part_ml_bytes(const oc::AttendParams& p) {
+  if (p.prefill) return align256((size_t)oc::prefill_partial_floats(p) / p.head_dim * 2 * sizeof(float));
+  return align256((size_t)oc::attend_max_items(p) * oc::kQG * 2 * sizeof(float));
+}
+
+size_t attend_ws(const oc::AttendParams& p) { return attend_part_o_bytes(p) + attend_part_ml_bytes(p); }
+
 void attend_bind_ws(oc::AttendParams& p, void* ws) {
-  const int64_t items = oc::attend_max_items(p);
   char* w = static_cast<char*>(ws);
   p.part_o = reinterpret_cast<float*>(w);
-  p.part_ml = reinterpret_cast<float*>(w + align256((size_t)items * oc::kQG * p.head_dim * sizeof(float)));
+  p.part_ml = reinterpret_cast<float*>(w + attend_part_o_bytes(p));
 }
 
 }  // namespace
@@ -218,6 +228,16 @@ size_t oc_attend_workspace_size(const oc_attend_args* a) {
   oc::AttendParams p;
   if (!a || make_attend_params(a, p)) return 0;
   return attend_ws(p);
+}
+
+int oc_attend_plan(const oc_attend_args* a, int32_t* kernel, int32_t* nsplit) {
+  if (!a || !kernel || !nsplit) return fail(OC_ERR_INVALID_ARGUMENT, "NULL argument");
+  oc::AttendParams p;
+  const int rc = make_attend_params(a, p);
+  if (rc) return rc;
+  *kernel = p.prefill ? OC_ATTEND_PREFILL_MFMA : OC_ATTEND_DECODE;
+  *nsplit = p.prefill ? p.nsplit : 0;
+  return OC_OK;
 }
 
 int oc_attend(const oc_attend_args* a, void* workspace, size_t workspace_bytes, void* stream) {

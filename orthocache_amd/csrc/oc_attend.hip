@@ -501,6 +501,7 @@ int64_t attend_max_items(const AttendParams& p) {
 }
 
 hipError_t launch_attend(const AttendParams& p, hipStream_t s) {
+  if (p.prefill) return launch_prefill(p, s);
   const int64_t max_items = attend_max_items(p);
   if (max_items > 0) {
     const int grid = (int)(max_items < kAttendGrid ? max_items : kAttendGrid);

@@ -143,8 +143,10 @@ struct AttendParams {
   const int* uniform;      // (num_segments, Hkv) or null: equal weights on every token
   float logit_scale;       // log2(e) / sqrt(head_dim)
   int chunk, nchunk;
-  float* part_o;    // (max_items, kQG, D)
-  float* part_ml;   // (max_items, kQG, 2)
+  float* part_o;    // decode: (max_items, kQG, D); prefill: (nsplit, segments, Hkv, D, rows_pad)
+  float* part_ml;   // decode: (max_items, kQG, 2); prefill: (nsplit, segments, Hkv, rows_pad, 2)
+  int prefill;      // 1: matrix-core prefill kernels (oc_prefill.hip)
+  int nsplit;       // prefill: ways the tile range of a list is split
   void* out;
   int out_dtype;
   int64_t out_seg_stride, out_tok_stride, out_head_stride;
@@ -155,5 +157,25 @@ int attend_nq_bucket(int nq_total);
 int attend_chunk(int dt, int head_dim, int nq_total);  // tokens per work item
 int64_t attend_max_items(const AttendParams& p);
 hipError_t launch_attend(const AttendParams& p, hipStream_t s);
+
+// ---------------------------------------------------------- oc_prefill.hip
+constexpr int kPrefillMinRows = 32;   // query rows per kv head from which the MFMA path is used
+constexpr int kPrefillMaxSplit = 16;
+
+constexpr int kPrefillRows = 128;     // query rows per prefill workgroup (4 waves x 32)
+
+__host__ __device__ inline int prefill_rows(const AttendParams& p) { return p.sq * p.group; }
+__host__ __device__ inline int prefill_qtiles(const AttendParams& p) {
+  return (prefill_rows(p) + kPrefillRows - 1) / kPrefillRows;
+}
+// Partial rows per (split, segment, kv head): the query tiles padded to 128.
+__host__ __device__ inline int64_t prefill_rows_pad(const AttendParams& p) {
+  return (int64_t)prefill_qtiles(p) * kPrefillRows;
+}
+
+bool prefill_supported(int kv_dtype, int q_dtype, int head_dim, int nq_rows, int block_size);
+int prefill_nsplit(const AttendParams& p);
+int64_t prefill_partial_floats(const AttendParams& p);
+hipError_t launch_prefill(const AttendParams& p, hipStream_t s);
 
 }  // namespace oc

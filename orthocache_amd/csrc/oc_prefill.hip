@@ -1,0 +1,402 @@
+// Indirect block-sparse attention, prefill form (many queries per kv head),
+// on the bf16/fp16 matrix cores.
+//
+// Same semantics as the decode form (oc_attend.hip) and the reference's
+// orthocache_attention loop (src/orthocache/adaptive_attention.py:46-184):
+// softmax(q.k / sqrt(d)) over the tokens of exactly the retained blocks, fp32
+// softmax state, output o / l; an empty list yields zeros.  Used when a kv head
+// has enough query rows (query tokens x heads of its group) that Q K^T and P V
+// are dense contractions (chunked prefill).
+//
+// Work decomposition: a workgroup (4 waves) takes 128 query rows of one
+// (segment, kv head) and a contiguous range of the list's 64-key tiles (the
+// tile range is split `nsplit` ways so the grid fills the chip); it writes a
+// partial (m, l, O) per row and prefill_combine_kernel merges the splits.
+//
+// Per wave: 32 query rows, one per lane pair (lane l and l^32 hold row l%32).
+// With v_mfma_f32_32x32x16 (A 32x16, B 16x32, fp32 C 32x32):
+//   S^T = K Q^T   A = K tile rows from LDS (16 B per lane), B = Q^T slice from
+//                 registers (loaded once), C lane l, i -> key 8(i/4)+4(l/32)+i%4,
+//                 query l%32;
+//   O^T += V^T P^T  A = V^T from a transposed LDS copy, B = P^T straight from
+//                 the S^T registers (converted to bf16/fp16), C -> d, query l%32.
+// So every query's softmax state (m, l) and its column of O^T stay in the two
+// lanes that own the query: no shuffles except one xor-32 per tile for the row
+// max.  The MFMA k index of P^T / V^T is a permutation of the 16 keys of a
+// slice (the keys a lane holds in S^T); the V^T copy in LDS stores keys in that
+// order so the A operand is one 16-byte read.
+//
+// LDS: K tile [64 keys][D] and V^T tile [D][64 keys], both with 16-byte blocks
+// XOR-swizzled by row so operand reads and the transposing writes spread over
+// the banks.  Global loads of the next tile are issued into registers before
+// the current tile's arithmetic.
+#include "oc_kernels.h"
+
+namespace oc {
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kPfWaves = 4;
+constexpr int kPfThreads = kPfWaves * kWave;
+constexpr int kPfRows = kPrefillRows;
+static_assert(kPfRows == kPfWaves * 32, "one 32-row MFMA tile per wave");
+constexpr int kPfKeys = 64;             // keys per tile
+
+template <int DT> struct Mma;
+template <> struct Mma<kBF16> {
+  __device__ __forceinline__ static f32x16_t run(u32x4_t a, u32x4_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static u32x4_t pack(const float* v) {
+    bf16x8_t r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = (__bf16)v[j];
+    return __builtin_bit_cast(u32x4_t, r);
+  }
+};
+template <> struct Mma<kF16> {
+  __device__ __forceinline__ static f32x16_t run(u32x4_t a, u32x4_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static u32x4_t pack(const float* v) {
+    f16x8_t r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = (_Float16)v[j];
+    return __builtin_bit_cast(u32x4_t, r);
+  }
+};
+
+__device__ __forceinline__ u32x4_t ld16v(const char* p) {
+  return *reinterpret_cast<const u32x4_t*>(p);
+}
+__device__ __forceinline__ u32x4_t ld16v_nt(const char* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+}
+
+// Position of key k (0..63) of a tile in the V^T rows: the 8 keys that lane
+// half hf supplies for MFMA k-slice s of S^T tile t are contiguous.
+__host__ __device__ constexpr int vt_pos(int k) {
+  const int t = k >> 5, s = (k >> 4) & 1, r = k & 15;
+  const int hf = (r >> 2) & 1, j = ((r >> 3) << 2) | (r & 3);
+  return (((t * 2 + s) * 2 + hf) << 3) | j;
+}
+
+// Swizzled byte offset of 16-byte block `blk` of row `row`.
+template <int ROW_BYTES>
+__device__ __forceinline__ int k_off(int row, int blk) {
+  return row * ROW_BYTES + ((blk ^ (row & 7)) << 4);
+}
+__device__ __forceinline__ int vt_off(int row, int byte_in_row) {
+  const int blk = byte_in_row >> 4;
+  return row * (kPfKeys * 2) + (((blk ^ ((row + (row >> 3)) & 7)) << 4) | (byte_in_row & 15));
+}
+
+}  // namespace
+
+bool prefill_supported(int kv_dtype, int q_dtype, int head_dim, int nq_rows, int block_size) {
+  return (kv_dtype == kBF16 || kv_dtype == kF16) && q_dtype == kv_dtype &&
+         (head_dim == 64 || head_dim == 128) && nq_rows >= kPrefillMinRows && block_size % kPfKeys == 0;
+}
+
+int prefill_nsplit(const AttendParams& p) {
+  const int64_t units = (int64_t)p.num_segments * p.num_kv_heads * prefill_qtiles(p);
+  const int64_t max_tiles = (int64_t)p.total_blocks * (p.block_size / kPfKeys);
+  int64_t ns = (2 * 256 + units - 1) / units;  // about two workgroups per CU
+  ns = ns < 1 ? 1 : (ns > kPrefillMaxSplit ? kPrefillMaxSplit : ns);
+  const int64_t by_tiles = max_tiles / 8 > 0 ? max_tiles / 8 : 1;  // at least ~8 tiles per split
+  return (int)(ns < by_tiles ? ns : by_tiles);
+}
+
+int64_t prefill_partial_floats(const AttendParams& p) {
+  return (int64_t)p.nsplit * p.num_segments * p.num_kv_heads * prefill_rows_pad(p) * p.head_dim;
+}
+
+template <int DT, int D>
+__global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendParams p) {
+  using M = Mma<DT>;
+  constexpr int DS = D / 16;                 // d slices of Q K^T
+  constexpr int DTN = D / 32;                // 32-row d tiles of O^T
+  constexpr int KROW = D * 2;                // bytes per K row in LDS
+  constexpr int KCH = kPfKeys * D / 8 / kPfThreads;  // 16-byte K chunks per thread
+  constexpr int KPT = D / 32;                // keys per thread in the V transpose (2 or 4)
+  constexpr int NDCH = D / 8;                // 16-byte chunks per row
+  static_assert(KCH >= 1 && (KPT == 2 || KPT == 4), "unsupported head_dim");
+
+  __shared__ __align__(16) char s_k[kPfKeys * KROW];
+  __shared__ __align__(16) char s_v[D * kPfKeys * 2];
+
+  const int nq_rows = prefill_rows(p);
+  const int nqt = (nq_rows + kPfRows - 1) / kPfRows;
+  int id = blockIdx.x;
+  const int qt = id % nqt; id /= nqt;
+  const int split = id % p.nsplit; id /= p.nsplit;
+  const int h = id % p.num_kv_heads;
+  const int seg = id / p.num_kv_heads;
+  const int list = seg * p.num_kv_heads + h;
+
+  const int count = p.per_head ? p.counts[list] : p.counts[seg];
+  const int tpb = p.block_size / kPfKeys;
+  const int ntiles = count * tpb;
+  const int per = (ntiles + p.nsplit - 1) / p.nsplit;
+  const int t0 = min(split * per, ntiles);
+  const int t1 = min(t0 + per, ntiles);
+  const bool uni = (p.uniform != nullptr) && (p.uniform[list] != 0);
+  const int off = p.cu_blocks ? p.cu_blocks[seg] : 0;
+  const int* idx = p.indices + (p.per_head ? (int64_t)h * p.total_blocks : 0) + off;
+
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int wave = t / kWave;
+  const int hf = lane >> 5;
+  const int q32 = lane & 31;
+
+  // Q^T slices (B operand): row r, 8 dims at 16 ds + 8 hf.
+  const int row = qt * kPfRows + wave * 32 + q32;
+  u32x4_t qf[DS];
+  {
+    const int rc = min(row, nq_rows - 1);
+    const int st = rc / p.group, g = rc - st * p.group;
+    const char* qp = reinterpret_cast<const char*>(p.q) +
+                     ((int64_t)seg * p.q_seg_stride + (int64_t)st * p.q_tok_stride +
+                      (int64_t)(h * p.group + g) * p.q_head_stride + 8 * hf) * 2;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) qf[ds] = ld16v(qp + ds * 32);
+  }
+
+  const int64_t krow_g = p.k_tok_stride * 2, vrow_g = p.v_tok_stride * 2;
+  const char* kbase = reinterpret_cast<const char*>(p.k) + (int64_t)h * p.k_head_stride * 2;
+  const char* vbase = reinterpret_cast<const char*>(p.v) + (int64_t)h * p.v_head_stride * 2;
+
+  // This thread's share of a tile: K chunks c = t + 256 u (key c / NDCH,
+  // chunk c % NDCH); V keys vk0 .. vk0 + KPT - 1 at chunk vdch.
+  const int vdch = t % NDCH;
+  const int vk0 = (t / NDCH) * KPT;
+  // Byte offsets inside a tile (64 token rows), fixed per thread.
+  int koff[KCH], voff[KPT];
+#pragma unroll
+  for (int u = 0; u < KCH; ++u) {
+    const int c = t + kPfThreads * u;
+    koff[u] = (int)((c / NDCH) * krow_g) + (c % NDCH) * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) voff[i] = (int)((vk0 + i) * vrow_g) + vdch * 16;
+  u32x4_t kr[KCH], vr[KPT];
+  auto load_tile = [&](int tau) {
+    const int blk = idx[tau / tpb];
+    const int64_t tok0 = (int64_t)(off + blk) * p.block_size + (int64_t)(tau % tpb) * kPfKeys;
+    const char* kt = kbase + tok0 * krow_g;
+    const char* vt = vbase + tok0 * vrow_g;
+#pragma unroll
+    for (int u = 0; u < KCH; ++u) kr[u] = ld16v_nt(kt + koff[u]);
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) vr[i] = ld16v_nt(vt + voff[i]);
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int u = 0; u < KCH; ++u) {
+      const int c = t + kPfThreads * u;
+      *reinterpret_cast<u32x4_t*>(s_k + k_off<KROW>(c / NDCH, c % NDCH)) = kr[u];
+    }
+    // V^T: element e of the chunk is dim 8 vdch + e; the KPT keys are
+    // adjacent in vt_pos order, so each dim takes one 4- or 8-byte write.
+    const int pb = vt_pos(vk0) * 2;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int w = e >> 1;
+      const bool hi = e & 1;
+      uint32_t pk[KPT / 2];
+#pragma unroll
+      for (int i = 0; i < KPT / 2; ++i) {
+        const uint32_t a = vr[2 * i][w], b = vr[2 * i + 1][w];
+        pk[i] = hi ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
+      }
+      char* dst = s_v + vt_off(8 * vdch + e, pb);
+      if constexpr (KPT == 4) {
+        *reinterpret_cast<uint2*>(dst) = make_uint2(pk[0], pk[1]);
+      } else {
+        *reinterpret_cast<uint32_t*>(dst) = pk[0];
+      }
+    }
+  };
+
+  f32x16_t o[DTN];
+#pragma unroll
+  for (int dt = 0; dt < DTN; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  const float c = p.logit_scale;
+
+  if (t0 < t1) load_tile(t0);
+  for (int tau = t0; tau < t1; ++tau) {
+    __syncthreads();  // the previous tile's operands have been read
+    store_tile();
+    __syncthreads();
+    if (tau + 1 < t1) load_tile(tau + 1);
+
+    // S^T for the two 32-key halves of the tile.
+    f32x16_t s[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[kt][i] = 0.f;
+      if (!uni) {
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+          const u32x4_t a = *reinterpret_cast<const u32x4_t*>(s_k + k_off<KROW>(kt * 32 + q32, 2 * ds + hf));
+          s[kt] = M::run(a, qf[ds], s[kt]);
+        }
+      }
+    }
+
+    // Online softmax for query q32 (both lane halves hold the same query).
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float m_new = fmaxf(m_run, mx * c);
+    const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+    float psum = 0.f;
+    float pv[2][16];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        pv[kt][i] = __builtin_amdgcn_exp2f(fmaf(s[kt][i], c, -m_new));
+        psum += pv[kt][i];
+      }
+    l_run = fmaf(l_run, alpha, psum);
+    m_run = m_new;
+    if (__ballot(alpha != 1.f)) {  // wave-uniform: skip the rescale when no row max moved
+#pragma unroll
+      for (int dt = 0; dt < DTN; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+    }
+
+    // O^T += V^T P^T over the four 16-key slices.
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl) {
+        const u32x4_t b = M::pack(&pv[kt][8 * sl]);
+        const int pb = (((kt * 2 + sl) * 2 + hf) << 4);
+#pragma unroll
+        for (int dt = 0; dt < DTN; ++dt) {
+          const u32x4_t a = *reinterpret_cast<const u32x4_t*>(s_v + vt_off(dt * 32 + q32, pb));
+          o[dt] = M::run(a, b, o[dt]);
+        }
+      }
+    }
+  }
+
+  // Partial for this split: m and l per row, O^T unnormalised.
+  const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+  const int64_t rows_pad = (int64_t)nqt * kPfRows;
+  const int64_t slab = ((int64_t)(split * p.num_segments + seg) * p.num_kv_heads + h);
+  if (hf == 0) {
+    p.part_ml[(slab * rows_pad + row) * 2] = m_run;
+    p.part_ml[(slab * rows_pad + row) * 2 + 1] = l_tot;
+  }
+  float* po = p.part_o + slab * D * rows_pad + row;
+#pragma unroll
+  for (int dt = 0; dt < DTN; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int d = dt * 32 + 8 * (i >> 2) + 4 * hf + (i & 3);
+      po[(int64_t)d * rows_pad] = o[dt][i];
+    }
+}
+
+// Merge the splits: one workgroup per (segment, kv head, 64 query rows).
+// Thread t handles row t % 64 and dims t / 64 + 4 j; the result goes through
+// LDS so the output rows are written with d fastest.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_combine_kernel(AttendParams p) {
+  __shared__ float s_o[64 * (D + 1)];
+  const int nq_rows = prefill_rows(p);
+  const int64_t rows_pad = prefill_rows_pad(p);
+  const int nrc = (int)(rows_pad / 64);
+  int id = blockIdx.x;
+  const int rc = id % nrc; id /= nrc;
+  const int h = id % p.num_kv_heads;
+  const int seg = id / p.num_kv_heads;
+  const int t = threadIdx.x;
+  const int r = t & 63;
+  const int dg = t >> 6;
+  const int64_t row = (int64_t)rc * 64 + r;
+  const int ns = p.nsplit;
+
+  float mm = -INFINITY;
+  for (int s = 0; s < ns; ++s) {
+    const int64_t slab = (int64_t)(s * p.num_segments + seg) * p.num_kv_heads + h;
+    mm = fmaxf(mm, p.part_ml[(slab * rows_pad + row) * 2]);
+  }
+  float w[kPrefillMaxSplit];
+  float ll = 0.f;
+#pragma unroll
+  for (int s = 0; s < kPrefillMaxSplit; ++s) {
+    w[s] = 0.f;
+    if (s < ns) {
+      const int64_t slab = (int64_t)(s * p.num_segments + seg) * p.num_kv_heads + h;
+      const float ms = p.part_ml[(slab * rows_pad + row) * 2];
+      w[s] = (ms == -INFINITY) ? 0.f : exp2f(ms - mm);
+      ll = fmaf(p.part_ml[(slab * rows_pad + row) * 2 + 1], w[s], ll);
+    }
+  }
+  const float inv = ll > 0.f ? 1.f / ll : 0.f;
+  for (int d = dg; d < D; d += 4) {
+    float acc = 0.f;
+#pragma unroll
+    for (int s = 0; s < kPrefillMaxSplit; ++s) {
+      if (s < ns) {
+        const int64_t slab = (int64_t)(s * p.num_segments + seg) * p.num_kv_heads + h;
+        acc = fmaf(w[s], p.part_o[(slab * D + d) * rows_pad + row], acc);
+      }
+    }
+    s_o[r * (D + 1) + d] = acc * inv;
+  }
+  __syncthreads();
+  for (int e = t; e < 64 * D; e += 256) {
+    const int rr = e / D, d = e - rr * D;
+    const int64_t qrow = (int64_t)rc * 64 + rr;
+    if (qrow < nq_rows) {
+      const int st = (int)(qrow / p.group), g = (int)(qrow - (int64_t)st * p.group);
+      const int64_t o = (int64_t)seg * p.out_seg_stride + (int64_t)st * p.out_tok_stride +
+                        (int64_t)(h * p.group + g) * p.out_head_stride + d;
+      store_elt(p.out_dtype, p.out, o, s_o[rr * (D + 1) + d]);
+    }
+  }
+}
+
+template <int DT, int D>
+static hipError_t launch_prefill_t(const AttendParams& p, hipStream_t s) {
+  const int nqt = prefill_qtiles(p);
+  const int64_t grid = (int64_t)p.num_segments * p.num_kv_heads * nqt * p.nsplit;
+  if (grid > 0) {
+    hipLaunchKernelGGL((attend_prefill_kernel<DT, D>), dim3((unsigned)grid), dim3(kPfThreads), 0, s, p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  const int64_t cgrid = (int64_t)p.num_segments * p.num_kv_heads * (prefill_rows_pad(p) / 64);
+  if (cgrid > 0) hipLaunchKernelGGL((prefill_combine_kernel<D>), dim3((unsigned)cgrid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill(const AttendParams& p, hipStream_t s) {
+  if (p.kv_dtype == kBF16) {
+    return p.head_dim == 64 ? launch_prefill_t<kBF16, 64>(p, s) : launch_prefill_t<kBF16, 128>(p, s);
+  }
+  return p.head_dim == 64 ? launch_prefill_t<kF16, 64>(p, s) : launch_prefill_t<kF16, 128>(p, s);
+}
+
+}  // namespace oc

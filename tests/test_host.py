@@ -101,6 +101,54 @@ def test_attend_workspace_rejects_bad_args(lib):
     assert lib.oc_attend(C.byref(a), None, 0, None) == -1
 
 
+def _plan_args(sq, hq, hkv, d, dtype, block=512, nb=256, q_dtype=None):
+    """AttendArgs with fake, aligned device addresses: oc_attend_plan only
+    validates and sizes, it never dereferences them."""
+    from orthocache_amd import _native as N
+
+    a = N.AttendArgs()
+    fake = 1 << 20
+    a.q = a.k = a.v = a.out = a.indices = a.counts = fake
+    a.q_dtype = dtype if q_dtype is None else q_dtype
+    a.kv_dtype = a.out_dtype = dtype
+    a.q_tok_stride, a.q_head_stride = hq * d, d
+    a.k_tok_stride = a.v_tok_stride = hkv * d
+    a.k_head_stride = a.v_head_stride = d
+    a.out_tok_stride, a.out_head_stride = hq * d, d
+    a.head_dim, a.num_kv_heads, a.group, a.sq = d, hkv, hq // hkv, sq
+    a.block_size, a.total_blocks, a.num_segments = block, nb, 1
+    return a
+
+
+@pytest.mark.parametrize("sq,hq,hkv,d,dt,block,qdt,expect", [
+    (512, 8, 8, 128, 1, 512, None, (1, 16)),   # C4: 32 (head, 128-row) tiles x 16 splits
+    (512, 8, 8, 128, 2, 512, None, (1, 16)),   # fp16
+    (512, 8, 8, 64, 1, 512, None, (1, 16)),
+    (16, 32, 8, 128, 1, 512, None, (1, 16)),   # 4 x 16 = 64 rows per kv head, one query tile
+    (32, 1, 1, 128, 1, 512, None, (1, 16)),    # threshold: 32 rows
+    (31, 1, 1, 128, 1, 512, None, (0, 0)),     # below it: decode kernel
+    (1, 32, 16, 256, 1, 512, None, (0, 0)),    # C2 decode
+    (512, 8, 8, 256, 1, 512, None, (0, 0)),    # head_dim 256: decode kernel
+    (512, 8, 8, 128, 0, 512, None, (0, 0)),    # fp32 K/V
+    (512, 8, 8, 128, 1, 512, 0, (0, 0)),       # fp32 q with bf16 K/V
+    (512, 8, 8, 128, 1, 100, None, (0, 0)),    # block not a multiple of 64
+])
+def test_attend_plan_routing(lib, sq, hq, hkv, d, dt, block, qdt, expect):
+    a = _plan_args(sq, hq, hkv, d, dt, block=block, nb=256 if block == 512 else 6, q_dtype=qdt)
+    kern, ns = C.c_int32(-1), C.c_int32(-1)
+    assert lib.oc_attend_plan(C.byref(a), C.byref(kern), C.byref(ns)) == 0, lib.oc_last_error()
+    assert (kern.value, ns.value) == expect
+
+
+def test_attend_plan_split_is_bounded_by_tiles(lib):
+    # 2 blocks x 8 tiles: at most 16 / 8 = 2 splits (about 8 tiles each).
+    a = _plan_args(512, 8, 8, 128, 1, nb=2)
+    kern, ns = C.c_int32(), C.c_int32()
+    assert lib.oc_attend_plan(C.byref(a), C.byref(kern), C.byref(ns)) == 0
+    assert (kern.value, ns.value) == (1, 2)
+    assert lib.oc_attend_plan(None, C.byref(kern), C.byref(ns)) == -1
+
+
 def _kernel_band_identity(block):
     """NumPy emulation of the scoring kernel's arithmetic for one (512, D) tile:
     bit-8 differences, a 4-point WHT over bits 6-7, and a centred low band."""
