@@ -445,3 +445,85 @@ class DecodeLayer:
             check(L.oc_attend(C.byref(ta), wsp, ws, stream_ptr(dev)), "oc_attend")
 
         return score, compact, attend
+
+
+class PrefillLayer:
+    """Pre-bound score -> query bounds -> compact -> attend for one chunk of
+    many queries on one segment (chunked prefill), fixed shapes and buffers.
+
+    q (Sq, Hq, D); keys/values (S, Hkv, D).  The bound of every query goes
+    through the tiled bound kernel; with bf16/fp16 inputs and head_dim 64 or
+    128 the attention runs on the matrix-core prefill kernels.  ``run()``
+    launches the four calls on the current stream without host
+    synchronisation; ``phases()`` returns them one at a time.
+    """
+
+    def __init__(self, q, k, v, tau, zeta_max, *, out=None, out_dtype=None):
+        require_gpu(q, k, v)
+        self.k = _kv_view(k, "keys")
+        self.v = _kv_view(v, "values")
+        self.q = _q_view(q, self.k.dtype)
+        if self.q.dim() != 3:
+            raise ValueError("q must be (seq_q, heads, head_dim)")
+        s, hkv, d = self.k.shape
+        if s % BLOCK:
+            raise ValueError(f"seq_len {s} is not a multiple of {BLOCK}")
+        nb = s // BLOCK
+        sq, hq, qd = self.q.shape
+        if qd != d:
+            raise ValueError(f"q head_dim {qd} != keys head_dim {d}")
+        group = kv_group(hq, hkv)
+        dev = self.k.device
+        self.device = dev
+        L = lib()
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.zeta = torch.empty((nb, hkv), **f32)
+        self.dc = torch.empty((nb, hkv, d), **f32)
+        self.e_ac = torch.empty((nb, hkv), **f32)
+        ntiles = int(L.oc_query_bound_tiles(sq, group))
+        self.tau_max = torch.empty((ntiles, nb, hkv), **f32)
+        self.indices = torch.empty((nb,), dtype=torch.int32, device=dev)
+        self.num_active = torch.empty((1,), dtype=torch.int32, device=dev)
+        self.out = out if out is not None else torch.empty(self.q.shape, dtype=out_dtype or q.dtype, device=dev)
+
+        sa = N.ScoreArgs()
+        sa.keys = ptr(self.k); sa.keys_dtype = dtype_code(self.k.dtype)
+        sa.keys_tok_stride = self.k.stride(0); sa.keys_head_stride = self.k.stride(1)
+        sa.head_dim = d; sa.num_kv_heads = hkv; sa.total_blocks = nb; sa.num_segments = 1
+        sa.zeta = ptr(self.zeta); sa.dc = ptr(self.dc); sa.e_ac = ptr(self.e_ac)
+        ba = N.BoundArgs(ptr(self.dc), ptr(self.e_ac), ptr(self.q), dtype_code(self.q.dtype), self.q.stride(0),
+                         self.q.stride(1), sq, group, d, hkv, nb, None, ptr(self.tau_max))
+        ca = N.CompactArgs()
+        ca.tau_max = ptr(self.tau_max); ca.tau_parts = ntiles; ca.zeta = ptr(self.zeta)
+        ca.tau = float(tau); ca.zeta_max = float(zeta_max)
+        ca.num_segments = 1; ca.num_kv_heads = hkv; ca.total_blocks = nb
+        ca.indices = ptr(self.indices); ca.num_active = ptr(self.num_active)
+        ta, _, _ = _attend_args(self.q, self.k, self.v, self.indices, self.num_active, out=self.out)
+        ws = int(L.oc_attend_workspace_size(C.byref(ta)))
+        if ws == 0:
+            check(L.oc_attend(C.byref(ta), None, 0, stream_ptr(dev)), "oc_attend")
+        self.workspace = torch.empty((ws,), dtype=torch.uint8, device=dev)
+        self.args = (sa, ba, ca, ta)
+        wsp = ptr(self.workspace)
+
+        def score():
+            check(L.oc_score_blocks(C.byref(sa), stream_ptr(dev)), "oc_score_blocks")
+
+        def bounds():
+            check(L.oc_query_bounds(C.byref(ba), stream_ptr(dev)), "oc_query_bounds")
+
+        def compact():
+            check(L.oc_mask_compact(C.byref(ca), stream_ptr(dev)), "oc_mask_compact")
+
+        def attend():
+            check(L.oc_attend(C.byref(ta), wsp, ws, stream_ptr(dev)), "oc_attend")
+
+        self._phases = (score, bounds, compact, attend)
+
+    def run(self) -> torch.Tensor:
+        for f in self._phases:
+            f()
+        return self.out
+
+    def phases(self):
+        return self._phases

@@ -241,19 +241,23 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
     __syncthreads();
     if (tau + 1 < t1) load_tile(tau + 1);
 
-    // S^T for the two 32-key halves of the tile.
+    // S^T for the two 32-key halves of the tile: all of a half's K operands
+    // are read from LDS before its MFMA chain.  Uniform lists take equal
+    // logits (a select, not a branch).
     f32x16_t s[2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
+      u32x4_t ka[DS];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s[kt][i] = 0.f;
-      if (!uni) {
+      for (int ds = 0; ds < DS; ++ds)
+        ka[ds] = *reinterpret_cast<const u32x4_t*>(s_k + k_off<KROW>(kt * 32 + q32, 2 * ds + hf));
+      f32x16_t acc;
 #pragma unroll
-        for (int ds = 0; ds < DS; ++ds) {
-          const u32x4_t a = *reinterpret_cast<const u32x4_t*>(s_k + k_off<KROW>(kt * 32 + q32, 2 * ds + hf));
-          s[kt] = M::run(a, qf[ds], s[kt]);
-        }
-      }
+      for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) acc = M::run(ka[ds], qf[ds], acc);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[kt][i] = uni ? 0.f : acc[i];
     }
 
     // Online softmax for query q32 (both lane halves hold the same query).
@@ -283,18 +287,19 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
         for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
     }
 
-    // O^T += V^T P^T over the four 16-key slices.
+    // O^T += V^T P^T over the four 16-key slices; a slice's V^T operands are
+    // read from LDS before its MFMAs.
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
       for (int sl = 0; sl < 2; ++sl) {
-        const u32x4_t b = M::pack(&pv[kt][8 * sl]);
         const int pb = (((kt * 2 + sl) * 2 + hf) << 4);
+        u32x4_t va[DTN];
 #pragma unroll
-        for (int dt = 0; dt < DTN; ++dt) {
-          const u32x4_t a = *reinterpret_cast<const u32x4_t*>(s_v + vt_off(dt * 32 + q32, pb));
-          o[dt] = M::run(a, b, o[dt]);
-        }
+        for (int dt = 0; dt < DTN; ++dt) va[dt] = *reinterpret_cast<const u32x4_t*>(s_v + vt_off(dt * 32 + q32, pb));
+        const u32x4_t b = M::pack(&pv[kt][8 * sl]);
+#pragma unroll
+        for (int dt = 0; dt < DTN; ++dt) o[dt] = M::run(va[dt], b, o[dt]);
       }
     }
   }
@@ -317,63 +322,69 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
     }
 }
 
-// Merge the splits: one workgroup per (segment, kv head, 64 query rows).
-// Thread t handles row t % 64 and dims t / 64 + 4 j; the result goes through
-// LDS so the output rows are written with d fastest.
+// Merge the splits: one workgroup per (segment, kv head, 64 query rows, 16
+// dims).  Thread t takes row t % 64 and dims 4 (t / 64) .. +3; every split's
+// (m, l) and o values are requested before any arithmetic (split indices
+// clamped, weights of missing splits zero), and the result goes through LDS
+// so output rows are written with d fastest.
+constexpr int kCombineDims = 16;
+
 template <int D>
 __global__ __launch_bounds__(256) void prefill_combine_kernel(AttendParams p) {
-  __shared__ float s_o[64 * (D + 1)];
+  constexpr int NS = kPrefillMaxSplit;
+  __shared__ float s_o[64 * (kCombineDims + 1)];
   const int nq_rows = prefill_rows(p);
   const int64_t rows_pad = prefill_rows_pad(p);
   const int nrc = (int)(rows_pad / 64);
+  constexpr int ndc = D / kCombineDims;
   int id = blockIdx.x;
+  const int dc = id % ndc; id /= ndc;
   const int rc = id % nrc; id /= nrc;
   const int h = id % p.num_kv_heads;
   const int seg = id / p.num_kv_heads;
   const int t = threadIdx.x;
   const int r = t & 63;
-  const int dg = t >> 6;
+  const int d0 = dc * kCombineDims + (t >> 6) * 4;
   const int64_t row = (int64_t)rc * 64 + r;
   const int ns = p.nsplit;
+  const int64_t slab_stride = (int64_t)p.num_segments * p.num_kv_heads;
+  const int64_t slab0 = (int64_t)seg * p.num_kv_heads + h;
 
-  float mm = -INFINITY;
-  for (int s = 0; s < ns; ++s) {
-    const int64_t slab = (int64_t)(s * p.num_segments + seg) * p.num_kv_heads + h;
-    mm = fmaxf(mm, p.part_ml[(slab * rows_pad + row) * 2]);
-  }
-  float w[kPrefillMaxSplit];
-  float ll = 0.f;
+  float mv[NS], lv[NS], ov[NS][4];
 #pragma unroll
-  for (int s = 0; s < kPrefillMaxSplit; ++s) {
-    w[s] = 0.f;
-    if (s < ns) {
-      const int64_t slab = (int64_t)(s * p.num_segments + seg) * p.num_kv_heads + h;
-      const float ms = p.part_ml[(slab * rows_pad + row) * 2];
-      w[s] = (ms == -INFINITY) ? 0.f : exp2f(ms - mm);
-      ll = fmaf(p.part_ml[(slab * rows_pad + row) * 2 + 1], w[s], ll);
+  for (int s = 0; s < NS; ++s) {
+    const int64_t slab = slab0 + (int64_t)min(s, ns - 1) * slab_stride;
+    const float2 ml = *reinterpret_cast<const float2*>(p.part_ml + (slab * rows_pad + row) * 2);
+    mv[s] = ml.x;
+    lv[s] = ml.y;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ov[s][j] = p.part_o[(slab * D + d0 + j) * rows_pad + row];
+  }
+  float mm = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) mm = fmaxf(mm, s < ns ? mv[s] : -INFINITY);
+  float ll = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const float w = (s >= ns || mv[s] == -INFINITY) ? 0.f : exp2f(mv[s] - mm);
+    if (w != 0.f) {
+      ll = fmaf(lv[s], w, ll);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = fmaf(ov[s][j], w, acc[j]);
     }
   }
   const float inv = ll > 0.f ? 1.f / ll : 0.f;
-  for (int d = dg; d < D; d += 4) {
-    float acc = 0.f;
 #pragma unroll
-    for (int s = 0; s < kPrefillMaxSplit; ++s) {
-      if (s < ns) {
-        const int64_t slab = (int64_t)(s * p.num_segments + seg) * p.num_kv_heads + h;
-        acc = fmaf(w[s], p.part_o[(slab * D + d) * rows_pad + row], acc);
-      }
-    }
-    s_o[r * (D + 1) + d] = acc * inv;
-  }
+  for (int j = 0; j < 4; ++j) s_o[r * (kCombineDims + 1) + (t >> 6) * 4 + j] = acc[j] * inv;
   __syncthreads();
-  for (int e = t; e < 64 * D; e += 256) {
-    const int rr = e / D, d = e - rr * D;
+  for (int e = t; e < 64 * kCombineDims; e += 256) {
+    const int rr = e / kCombineDims, dd = e - rr * kCombineDims;
     const int64_t qrow = (int64_t)rc * 64 + rr;
     if (qrow < nq_rows) {
       const int st = (int)(qrow / p.group), g = (int)(qrow - (int64_t)st * p.group);
       const int64_t o = (int64_t)seg * p.out_seg_stride + (int64_t)st * p.out_tok_stride +
-                        (int64_t)(h * p.group + g) * p.out_head_stride + d;
-      store_elt(p.out_dtype, p.out, o, s_o[rr * (D + 1) + d]);
+                        (int64_t)(h * p.group + g) * p.out_head_stride + dc * kCombineDims + dd;
+      store_elt(p.out_dtype, p.out, o, s_o[rr * (kCombineDims + 1) + dd]);
     }
   }
 }
@@ -387,7 +398,7 @@ static hipError_t launch_prefill_t(const AttendParams& p, hipStream_t s) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  const int64_t cgrid = (int64_t)p.num_segments * p.num_kv_heads * (prefill_rows_pad(p) / 64);
+  const int64_t cgrid = (int64_t)p.num_segments * p.num_kv_heads * (prefill_rows_pad(p) / 64) * (D / kCombineDims);
   if (cgrid > 0) hipLaunchKernelGGL((prefill_combine_kernel<D>), dim3((unsigned)cgrid), dim3(256), 0, s, p);
   return hipGetLastError();
 }
