@@ -116,7 +116,7 @@ int oc_score_blocks(const oc_score_args* a, void* stream);
 
 /* Query-aware bound for many queries of one segment (prefill), from the dc
  * and e_ac outputs of oc_score_blocks.  bounds: (sq*group, nb, Hkv) with query
- * row t*group + g (the GQA-folded layout); tau_part: (ceil(sq*group/32), nb,
+ * row t*group + g (the GQA-folded layout); tau_part: (ceil(sq*group/64), nb,
  * Hkv) partial maxima for oc_mask_compact (tau_parts = that count).
  * Replaces compute_query_aware_bounds (src/orthocache/spectral_energy.py:141-177). */
 typedef struct oc_bound_args {

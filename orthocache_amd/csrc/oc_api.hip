@@ -106,7 +106,10 @@ int oc_score_blocks(const oc_score_args* a, void* stream) {
   return hip_check(oc::launch_score(p, (hipStream_t)stream), "oc_score_blocks");
 }
 
-int32_t oc_query_bound_tiles(int32_t sq, int32_t group) { return (sq * group + 31) / 32; }
+int32_t oc_query_bound_tiles(int32_t sq, int32_t group) {
+  const int qt = oc::bound_query_tile();
+  return (sq * group + qt - 1) / qt;
+}
 
 int oc_query_bounds(const oc_bound_args* a, void* stream) {
   if (!a) return fail(OC_ERR_INVALID_ARGUMENT, "args is NULL");
@@ -114,7 +117,8 @@ int oc_query_bounds(const oc_bound_args* a, void* stream) {
   if (!valid_dtype(a->q_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "q: unknown dtype");
   if (a->head_dim <= 0 || a->head_dim > 1024 || a->num_kv_heads <= 0 || a->num_blocks < 0 || a->sq < 0 || a->group <= 0)
     return fail(OC_ERR_INVALID_ARGUMENT, "bad shape");
-  const int64_t grid = (int64_t)oc_query_bound_tiles(a->sq, a->group) * ((a->num_blocks + 7) / 8) * a->num_kv_heads;
+  const int bbt = oc::bound_block_tile();
+  const int64_t grid = (int64_t)oc_query_bound_tiles(a->sq, a->group) * ((a->num_blocks + bbt - 1) / bbt) * a->num_kv_heads;
   if (grid > 0x7fffffffLL) return fail(OC_ERR_UNSUPPORTED, "too many tiles");
   oc::BoundParams p{a->dc, a->e_ac, a->q, a->q_dtype, a->q_tok_stride, a->q_head_stride, a->sq, a->group,
                     a->head_dim, a->num_kv_heads, a->num_blocks, a->bounds, a->tau_part};

@@ -126,13 +126,23 @@ __device__ inline void compact_segment(const CompactParams& p, int seg, uint8_t*
             tv[u] = p.tau_max[g0 + e];
             zv[u] = zsrc[g0 + e];
           }
-          for (int part = 1; part < p.tau_parts; ++part) {
-            const float* tp = p.tau_max + (int64_t)part * p.total_blocks * H + g0;
-            float pv[kEpt];
+          // Further partial maxima (one per query tile), kPB parts requested
+          // together; a clamped repeat of the last part is harmless (max is
+          // idempotent).
+          constexpr int kPB = 8;
+          for (int part = 1; part < p.tau_parts; part += kPB) {
+            float pv[kPB][kEpt];
 #pragma unroll
-            for (int u = 0; u < kEpt; ++u) pv[u] = tp[min(e0 + u * (int)blockDim.x + t, ne - 1)];
+            for (int b = 0; b < kPB; ++b) {
+              const int pp = min(part + b, p.tau_parts - 1);
+              const float* tp = p.tau_max + (int64_t)pp * p.total_blocks * H + g0;
 #pragma unroll
-            for (int u = 0; u < kEpt; ++u) tv[u] = nanmax(tv[u], pv[u]);
+              for (int u = 0; u < kEpt; ++u) pv[b][u] = tp[min(e0 + u * (int)blockDim.x + t, ne - 1)];
+            }
+#pragma unroll
+            for (int b = 0; b < kPB; ++b)
+#pragma unroll
+              for (int u = 0; u < kEpt; ++u) tv[u] = nanmax(tv[u], pv[b][u]);
           }
 #pragma unroll
           for (int u = 0; u < kEpt; ++u) kk[u] = (tv[u] >= tau) & ((p.zeta == nullptr) | (zv[u] <= zmax));

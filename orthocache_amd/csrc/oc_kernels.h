@@ -49,6 +49,8 @@ struct EnergyParams {
   float* out;
 };
 
+int bound_query_tile();  // queries per partial maximum of the bound kernel
+int bound_block_tile();
 hipError_t launch_bound(const BoundParams& p, hipStream_t s);
 hipError_t launch_block_energy(const EnergyParams& p, hipStream_t s);
 

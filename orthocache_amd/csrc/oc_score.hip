@@ -248,69 +248,116 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
 }
 
 // Query-aware bound for many queries (prefill): one workgroup per
-// (query tile of 32, block tile of 8, kv head).  Needs kbar (from dc) and
-// E_AC from score_kernel.  Writes the full bound tensor (Sq*G, nb, Hkv) and/or
-// the per-query-tile NaN-propagating max (ntiles, nb, Hkv).
-constexpr int kBoundQT = 32;
-constexpr int kBoundBT = 8;
+// (64 queries, 64 blocks, kv head).  Needs kbar (from dc) and E_AC from
+// score_kernel.  Writes the full bound tensor (Sq*G, nb, Hkv) and/or the
+// per-query-tile NaN-propagating max (ntiles, nb, Hkv), ntiles = ceil(Sq*G/64).
+//
+// q and kbar are staged in LDS transposed ([d][query], [d][block], fp32) in
+// chunks of 64 dims; each thread holds a 4 x 4 (query x block) tile of dot
+// products plus its 4 queries' squared norms, so one pair of 16-byte LDS reads
+// feeds 20 FMAs.  Every dot product accumulates over d in order, as a plain
+// loop would.
+constexpr int kBoundQT = 64;
+constexpr int kBoundBT = 64;
+constexpr int kBoundDC = 64;
+constexpr int kBoundPad = 4;
 
+template <int QDT>
 __global__ __launch_bounds__(256) void bound_kernel(BoundParams p) {
-  extern __shared__ float smem[];
+  using EQ = Elt<QDT>;
+  __shared__ __align__(16) float s_q[kBoundDC][kBoundQT + kBoundPad];
+  __shared__ __align__(16) float s_k[kBoundDC][kBoundBT + kBoundPad];
   const int D = p.head_dim;
-  const int DP = D + 1;
-  float* s_q = smem;                       // kBoundQT x DP
-  float* s_k = smem + kBoundQT * DP;       // kBoundBT x DP
+  const int H = p.num_kv_heads;
+  const int nb = p.num_blocks;
   const int nq = p.sq * p.group;
-  const int nqt = (nq + kBoundQT - 1) / kBoundQT;
-  const int nbt = (p.num_blocks + kBoundBT - 1) / kBoundBT;
+  const int nbt = (nb + kBoundBT - 1) / kBoundBT;
   int id = blockIdx.x;
-  const int h = id % p.num_kv_heads; id /= p.num_kv_heads;
+  const int h = id % H; id /= H;
   const int bt = id % nbt;
   const int qt = id / nbt;
-  if (qt >= nqt) return;
   const int t = threadIdx.x;
-  for (int e = t; e < kBoundQT * D; e += blockDim.x) {
-    const int r = e / D, d = e - r * D;
-    const int qi = qt * kBoundQT + r;
-    float v = 0.f;
-    if (qi < nq) {
-      const int st = qi / p.group, g = qi - st * p.group;
-      v = load_elt(p.q_dtype, p.q, (int64_t)st * p.q_tok_stride + (int64_t)(h * p.group + g) * p.q_head_stride + d);
+
+  // Staging role: query / block row r of the tile, dims e0 + 4 j of a chunk.
+  const int r = t & 63, e0 = t >> 6;
+  const int qs = qt * kBoundQT + r;
+  const bool q_ok = qs < nq;
+  const int qc = min(qs, nq - 1);
+  const int st = qc / p.group, gq = qc - st * p.group;
+  const int64_t qoff = (int64_t)st * p.q_tok_stride + (int64_t)(h * p.group + gq) * p.q_head_stride;
+  const int bs = bt * kBoundBT + r;
+  const bool b_ok = bs < nb;
+  const float* dcrow = p.dc + ((int64_t)min(bs, nb - 1) * H + h) * D;
+
+  // Compute role: queries 4 tq .. +3, blocks 4 tb .. +3 of the tile.
+  const int tq = t & 15, tb = t >> 4;
+  float eac[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) eac[j] = p.e_ac[(int64_t)min(bt * kBoundBT + 4 * tb + j, nb - 1) * H + h];
+  float acc[4][4], qq[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    qq[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+  }
+
+  for (int d0 = 0; d0 < D; d0 += kBoundDC) {
+    float qv[16], kv[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int d = min(d0 + e0 + 4 * j, D - 1);
+      qv[j] = EQ::load1(p.q, qoff + d);
+      kv[j] = dcrow[d];
     }
-    s_q[r * DP + d] = v;
+    __syncthreads();  // the previous chunk has been consumed
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const bool ok = d0 + e0 + 4 * j < D;
+      s_q[e0 + 4 * j][r] = (ok && q_ok) ? qv[j] : 0.f;
+      s_k[e0 + 4 * j][r] = (ok && b_ok) ? kv[j] / kSqrt512 : 0.f;  // kbar, spectral_energy.py:166
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int dd = 0; dd < kBoundDC; ++dd) {
+      const float4 a = *reinterpret_cast<const float4*>(&s_q[dd][4 * tq]);
+      const float4 b = *reinterpret_cast<const float4*>(&s_k[dd][4 * tb]);
+      const float av[4] = {a.x, a.y, a.z, a.w};
+      const float bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        qq[i] = fmaf(av[i], av[i], qq[i]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+      }
+    }
   }
-  for (int e = t; e < kBoundBT * D; e += blockDim.x) {
-    const int r = e / D, d = e - r * D;
-    const int b = bt * kBoundBT + r;
-    s_k[r * DP + d] = (b < p.num_blocks) ? p.dc[((int64_t)b * p.num_kv_heads + h) * D + d] / kSqrt512 : 0.f;
-  }
-  __syncthreads();
-  const int ql = t % kBoundQT;
-  const int bl = t / kBoundQT;   // 0..7
-  const int qi = qt * kBoundQT + ql;
-  const int b = bt * kBoundBT + bl;
-  float dot = 0.f, qq = 0.f;
-  for (int d = 0; d < D; ++d) {
-    const float qv = s_q[ql * DP + d];
-    dot = fmaf(qv, s_k[bl * DP + d], dot);
-    qq = fmaf(qv, qv, qq);
-  }
-  const bool valid = (qi < nq) && (b < p.num_blocks);
-  float bound = -INFINITY;
-  if (valid) {
-    const float sqrt_d = sqrtf((float)D);
-    const float eac = p.e_ac[(int64_t)b * p.num_kv_heads + h];
-    bound = dot / sqrt_d + (sqrtf(qq) * sqrtf(eac)) / sqrt_d;
-    if (p.bounds) p.bounds[((int64_t)qi * p.num_blocks + b) * p.num_kv_heads + h] = bound;
+
+  // tau_j(q) = q.kbar/sqrt(d) + ||q|| sqrt(E_AC)/sqrt(d) (spectral_energy.py:170-176);
+  // NaN-propagating max over the tile's queries.
+  const float sqrt_d = sqrtf((float)D);
+  float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int qi = qt * kBoundQT + 4 * tq + i;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int b = bt * kBoundBT + 4 * tb + j;
+      if (qi < nq && b < nb) {
+        const float bound = acc[i][j] / sqrt_d + (sqrtf(qq[i]) * sqrtf(eac[j])) / sqrt_d;
+        if (p.bounds) p.bounds[((int64_t)qi * nb + b) * H + h] = bound;
+        m[j] = nanmax(m[j], bound);
+      }
+    }
   }
   if (p.tau_part) {
-    // NaN-propagating max over the 32 queries of this tile (lanes ql share bl
-    // within one wave: 64 lanes = 2 block rows x 32 queries).
-    float m = bound;
 #pragma unroll
-    for (int o = kBoundQT / 2; o > 0; o >>= 1) m = nanmax(m, __shfl_xor(m, o, kBoundQT));
-    if (ql == 0 && b < p.num_blocks)
-      p.tau_part[((int64_t)qt * p.num_blocks + b) * p.num_kv_heads + h] = m;
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) m[j] = nanmax(m[j], __shfl_xor(m[j], o, 16));
+      const int b = bt * kBoundBT + 4 * tb + j;
+      if (tq == 0 && b < nb) p.tau_part[((int64_t)qt * nb + b) * H + h] = m[j];
+    }
   }
 }
 
@@ -389,15 +436,18 @@ hipError_t launch_bound(const BoundParams& p, hipStream_t s) {
   if (nq == 0 || p.num_blocks == 0) return hipSuccess;
   const int nqt = (nq + kBoundQT - 1) / kBoundQT;
   const int nbt = (p.num_blocks + kBoundBT - 1) / kBoundBT;
-  const size_t lds = (size_t)(kBoundQT + kBoundBT) * (p.head_dim + 1) * sizeof(float);
-  if (lds > 65536) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bound_kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
+  const dim3 grid(nqt * nbt * p.num_kv_heads);
+  switch (p.q_dtype) {
+    case kF32: hipLaunchKernelGGL(bound_kernel<kF32>, grid, dim3(256), 0, s, p); break;
+    case kBF16: hipLaunchKernelGGL(bound_kernel<kBF16>, grid, dim3(256), 0, s, p); break;
+    case kF16: hipLaunchKernelGGL(bound_kernel<kF16>, grid, dim3(256), 0, s, p); break;
+    default: return hipErrorInvalidValue;
   }
-  hipLaunchKernelGGL(bound_kernel, dim3(nqt * nbt * p.num_kv_heads), dim3(256), lds, s, p);
   return hipGetLastError();
 }
+
+int bound_query_tile() { return kBoundQT; }
+int bound_block_tile() { return kBoundBT; }
 
 hipError_t launch_block_energy(const EnergyParams& p, hipStream_t s) {
   if (p.num_blocks == 0) return hipSuccess;

@@ -90,7 +90,8 @@ def test_validation_errors_without_gpu(lib):
     assert lib.oc_copy_blocks(16, 16, 16, 16, 1, 100, 0, None) == -1  # not a multiple of 16
     assert lib.oc_band_energy(16, 1, 1, 1, 10, 5, 16, None) == -1  # s0 > s1
     assert lib.oc_query_bound_tiles(2, 16) == 1
-    assert lib.oc_query_bound_tiles(512, 1) == 16
+    assert lib.oc_query_bound_tiles(512, 1) == 8
+    assert lib.oc_query_bound_tiles(65, 1) == 2
 
 
 def test_attend_workspace_rejects_bad_args(lib):
