@@ -76,9 +76,6 @@ template <> struct Mma<kF16> {
 __device__ __forceinline__ u32x4_t ld16v(const char* p) {
   return *reinterpret_cast<const u32x4_t*>(p);
 }
-__device__ __forceinline__ u32x4_t ld16v_nt(const char* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
-}
 
 // Position of key k (0..63) of a tile in the V^T rows: the 8 keys that lane
 // half hf supplies for MFMA k-slice s of S^T tile t are contiguous.
@@ -134,7 +131,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
 
   const int nq_rows = prefill_rows(p);
   const int nqt = (nq_rows + kPfRows - 1) / kPfRows;
+  // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs,
+  // so the query tiles of one (segment, kv head, split) -- which read the same
+  // K/V tiles -- are given consecutive slots on one XCD and share its L2.
   int id = blockIdx.x;
+  if ((gridDim.x & 7) == 0) id = (id & 7) * (int)(gridDim.x >> 3) + (id >> 3);
   const int qt = id % nqt; id /= nqt;
   const int split = id % p.nsplit; id /= p.nsplit;
   const int h = id % p.num_kv_heads;
@@ -194,9 +195,9 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
     const char* kt = kbase + tok0 * krow_g;
     const char* vt = vbase + tok0 * vrow_g;
 #pragma unroll
-    for (int u = 0; u < KCH; ++u) kr[u] = ld16v_nt(kt + koff[u]);
+    for (int u = 0; u < KCH; ++u) kr[u] = ld16v(kt + koff[u]);
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) vr[i] = ld16v_nt(vt + voff[i]);
+    for (int i = 0; i < KPT; ++i) vr[i] = ld16v(vt + voff[i]);
   };
   auto store_tile = [&]() {
 #pragma unroll
@@ -241,24 +242,22 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
     __syncthreads();
     if (tau + 1 < t1) load_tile(tau + 1);
 
-    // S^T for the two 32-key halves of the tile: all of a half's K operands
-    // are read from LDS before its MFMA chain.  Uniform lists take equal
-    // logits (a select, not a branch).
+    // S^T for the two 32-key halves of the tile, the two MFMA chains
+    // interleaved over the d slices.  Uniform lists take equal logits (a
+    // select, not a branch).
+    f32x16_t acc0, acc1;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) { acc0[i] = 0.f; acc1[i] = 0.f; }
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      const u32x4_t a0 = *reinterpret_cast<const u32x4_t*>(s_k + k_off<KROW>(q32, 2 * ds + hf));
+      const u32x4_t a1 = *reinterpret_cast<const u32x4_t*>(s_k + k_off<KROW>(32 + q32, 2 * ds + hf));
+      acc0 = M::run(a0, qf[ds], acc0);
+      acc1 = M::run(a1, qf[ds], acc1);
+    }
     f32x16_t s[2];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      u32x4_t ka[DS];
-#pragma unroll
-      for (int ds = 0; ds < DS; ++ds)
-        ka[ds] = *reinterpret_cast<const u32x4_t*>(s_k + k_off<KROW>(kt * 32 + q32, 2 * ds + hf));
-      f32x16_t acc;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-#pragma unroll
-      for (int ds = 0; ds < DS; ++ds) acc = M::run(ka[ds], qf[ds], acc);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[kt][i] = uni ? 0.f : acc[i];
-    }
+    for (int i = 0; i < 16; ++i) { s[0][i] = uni ? 0.f : acc0[i]; s[1][i] = uni ? 0.f : acc1[i]; }
 
     // Online softmax for query q32 (both lane halves hold the same query).
     float mx = -INFINITY;
