@@ -42,8 +42,9 @@ def parse():
     p.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="first run a plain device copy of this many MiB (reference for HBM counters)")
-    p.add_argument("--workload", choices=("c2", "c4"), default="c2",
-                   help="c2: the headline decode layer (default); c4: chunked prefill on the matrix cores")
+    p.add_argument("--workload", choices=("c2", "c3", "c4", "c5"), default="c2",
+                   help="c2: the headline decode layer (default); c3: ragged batched decode; "
+                        "c4: chunked prefill on the matrix cores; c5: 60-layer scoring sweep")
     return p.parse_args()
 
 
@@ -135,8 +136,8 @@ def main():
     dev = torch.device("cuda:0")
     print(f"bench: lib {_native.LIB_PATH}", file=sys.stderr, flush=True)
 
-    if args.workload == "c4":
-        run_c4(args, torch, dev)
+    if args.workload != "c2":
+        {"c3": run_c3, "c4": run_c4, "c5": run_c5}[args.workload](args, torch, dev)
         return
 
     if args.copy_probe_mib:
@@ -276,6 +277,98 @@ def run_c4(args, torch, dev):
                      "frac": round(tflops / peak, 4), "traffic": None},
     }
     print(json.dumps(result), flush=True)
+
+
+def _line(metric, us, args, config, extra):
+    r = {"metric": metric, "value": round(us, 2), "unit": "us", "n_gpus": 1, "steps": args.steps,
+         "warmup": args.warmup, "ms_per_step": round(us / 1000.0, 5), "higher_is_better": False,
+         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+         "data": "synthetic (seeded N(0,1) K/V + block offsets, 10% noise blocks, generated on the GPU)",
+         "config": config}
+    r.update(extra)
+    return r
+
+
+def _per_segment_thresholds(torch, tm, z, cu_blocks, evicts):
+    from orthocache_amd import workloads
+
+    taus, zmaxs = [], []
+    for s, ev in enumerate(evicts):
+        lo, hi = int(cu_blocks[s]), int(cu_blocks[s + 1])
+        t, zm = workloads.calibrate_unified(tm[lo:hi], z[lo:hi], ev)
+        taus.append(t)
+        zmaxs.append(zm)
+    dev = tm.device
+    return (torch.tensor(taus, dtype=torch.float32, device=dev), torch.tensor(zmaxs, dtype=torch.float32, device=dev))
+
+
+def run_c3(args, torch, dev):
+    """C3: batch 32 ragged decode, 32 query / 8 kv
+    heads, d=128, lengths uniform in [4096, 32768] (multiples of 512), each
+    sequence with its own eviction rate in [30%, 95%].  A step is one fused
+    layer over the whole batch (one scoring launch, one compaction launch with
+    one workgroup per sequence, attention + combine)."""
+    from orthocache_amd import _ops, varlen, workloads
+
+    wl = workloads.c3(dev)
+    cu_b = (wl.cu_seqlens // 512).cpu().numpy()
+    tm, z = varlen.score_varlen(wl.q, wl.k, wl.cu_seqlens)
+    tau_t, zmax_t = _per_segment_thresholds(torch, tm, z, cu_b, wl.meta["evict"])
+    nseg = len(wl.meta["lens"])
+    layer = _ops.DecodeLayer(wl.q, wl.k, wl.v, tau_t, zmax_t, cu_blocks=varlen.cu_blocks_from_seqlens(wl.cu_seqlens),
+                             num_segments=nseg)
+    for _ in range(args.warmup):
+        layer.run()
+    torch.cuda.synchronize()
+    active = layer.num_active.cpu().numpy()
+    us = event_time_us(layer.run, args.steps, torch)
+    s, hkv, d = wl.k.shape
+    hq = wl.q.shape[-2]
+    kept = int(active.sum())
+    q_bytes = wl.q.numel() * 2
+    score_bytes = s * hkv * d * 2 + q_bytes + (s // 512) * hkv * 8
+    attend_bytes = kept * 512 * hkv * d * 2 * 2 + q_bytes + wl.q.numel() * 2
+    total = score_bytes + attend_bytes
+    gbs = total / (us * 1e-6) / 1e9
+    print(json.dumps(_line("us per batched decode layer score+compact+attend, C3 ragged batch 32",
+                           us, args,
+                           {"workload": wl.name, "batch": nseg, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
+                            "tokens": s, "blocks": s // 512, "retained_blocks": kept,
+                            "evict_range": [0.30, 0.95]},
+                           {"algorithmic_bytes": total, "layer_gbps": round(gbs, 1),
+                            "layer_frac_of_peak": round(gbs / PEAK_HBM_GBS, 4)})), flush=True)
+
+
+def run_c5(args, torch, dev):
+    """C5: 60-layer scoring sweep with no attention:
+    50 sliding-window layers of 1024 tokens and 10 global layers of 65536, 16
+    kv heads, d=256, bf16 keys.  A step is one sweep: one scoring launch over
+    all layers as segments (FWHT bands, zeta, inline bound of each layer's 32
+    query heads) and one mask + compaction launch, at 90% eviction."""
+    from orthocache_amd import varlen, workloads
+
+    wl = workloads.c5(dev)
+    cu_b = (wl.cu_seqlens // 512).cpu().numpy()
+    tm, z = varlen.score_varlen(wl.q, wl.k, wl.cu_seqlens)
+    nl = len(wl.meta["lens"])
+    tau_t, zmax_t = _per_segment_thresholds(torch, tm, z, cu_b, [0.9] * nl)
+
+    def sweep():
+        t2, z2 = varlen.score_varlen(wl.q, wl.k, wl.cu_seqlens)
+        return varlen.mask_compact_varlen(t2, z2, wl.cu_seqlens, tau_t, zmax_t)
+
+    for _ in range(args.warmup):
+        sweep()
+    torch.cuda.synchronize()
+    us = event_time_us(sweep, args.steps, torch)
+    s, hkv, d = wl.k.shape
+    score_bytes = s * hkv * d * 2 + wl.q.numel() * 2 + (s // 512) * hkv * 8
+    gbs = score_bytes / (us * 1e-6) / 1e9
+    print(json.dumps(_line("us per 60-layer scoring sweep (score + mask + compaction), C5", us, args,
+                           {"workload": wl.name, "layers": nl, "kv_heads": hkv, "head_dim": d, "tokens": s,
+                            "blocks": s // 512, "evict": 0.9},
+                           {"algorithmic_bytes": score_bytes, "sweep_gbps": round(gbs, 1),
+                            "sweep_frac_of_peak": round(gbs / PEAK_HBM_GBS, 4)})), flush=True)
 
 
 if __name__ == "__main__":

@@ -46,6 +46,7 @@ constexpr int kPfThreads = kPfWaves * kWave;
 constexpr int kPfRows = kPrefillRows;
 static_assert(kPfRows == kPfWaves * 32, "one 32-row MFMA tile per wave");
 constexpr int kPfKeys = 64;             // keys per tile
+constexpr float kLazy = 8.f;            // log2 headroom before the softmax reference moves
 
 template <int DT> struct Mma;
 template <> struct Mma<kBF16> {
@@ -88,7 +89,8 @@ __host__ __device__ constexpr int vt_pos(int k) {
 // Swizzled byte offset of 16-byte block `blk` of row `row`.
 template <int ROW_BYTES>
 __device__ __forceinline__ int k_off(int row, int blk) {
-  return row * ROW_BYTES + ((blk ^ (row & 7)) << 4);
+  constexpr int mask = (ROW_BYTES / 16 < 16 ? ROW_BYTES / 16 : 16) - 1;
+  return row * ROW_BYTES + ((blk ^ (row & mask)) << 4);
 }
 __device__ __forceinline__ int vt_off(int row, int byte_in_row) {
   const int blk = byte_in_row >> 4;
@@ -177,8 +179,19 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
 
   // This thread's share of a tile: K chunks c = t + 256 u (key c / NDCH,
   // chunk c % NDCH); V keys vk0 .. vk0 + KPT - 1 at chunk vdch.
-  const int vdch = t % NDCH;
-  const int vk0 = (t / NDCH) * KPT;
+  // Lane -> (16-byte chunk, key group) of the V transpose.  For head_dim 128
+  // the 16 lanes of an LDS write phase cover 8 dims x 2 key groups whose
+  // positions differ in the 8-byte half of a block, so the writes spread over
+  // all banks; each key row is still read as 256 contiguous bytes.
+  int vdch, vgrp;
+  if constexpr (NDCH == 16) {
+    vdch = (t & 7) | (((t >> 4) & 1) << 3);
+    vgrp = (t >> 6) * 4 + ((t >> 3) & 1) * 2 + ((t >> 5) & 1);
+  } else {
+    vdch = t % NDCH;
+    vgrp = t / NDCH;
+  }
+  const int vk0 = vgrp * KPT;
   // Byte offsets inside a tile (64 token rows), fixed per thread.
   int koff[KCH], voff[KPT];
 #pragma unroll
@@ -255,9 +268,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
       acc0 = M::run(a0, qf[ds], acc0);
       acc1 = M::run(a1, qf[ds], acc1);
     }
-    f32x16_t s[2];
+    f32x16_t s[2] = {acc0, acc1};
+    if (uni) {  // wave-uniform and rare: equal logits
 #pragma unroll
-    for (int i = 0; i < 16; ++i) { s[0][i] = uni ? 0.f : acc0[i]; s[1][i] = uni ? 0.f : acc1[i]; }
+      for (int i = 0; i < 16; ++i) { s[0][i] = 0.f; s[1][i] = 0.f; }
+    }
 
     // Online softmax for query q32 (both lane halves hold the same query).
     float mx = -INFINITY;
@@ -266,7 +281,13 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
 #pragma unroll
       for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][i]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float m_new = fmaxf(m_run, mx * c);
+    // Lazy rescale: the reference point m_run moves only when the tile max
+    // exceeds it by more than 2^kLazy (weights stay <= 2^kLazy, exact in fp32
+    // and in the bf16/fp16 P operand); l and O use the same reference, so the
+    // quotient o / l is unchanged.  Most tiles then skip the O rescale.
+    const float m_tile = mx * c;
+    const bool move = !(m_tile <= m_run + kLazy);  // also true for the first tile (m_run = -inf)
+    const float m_new = move ? fmaxf(m_run, m_tile) : m_run;
     const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
     float psum = 0.f;
     float pv[2][16];
@@ -279,7 +300,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
       }
     l_run = fmaf(l_run, alpha, psum);
     m_run = m_new;
-    if (__ballot(alpha != 1.f)) {  // wave-uniform: skip the rescale when no row max moved
+    if (__ballot(move)) {  // wave-uniform
 #pragma unroll
       for (int dt = 0; dt < DTN; ++dt)
 #pragma unroll
