@@ -42,9 +42,10 @@ def parse():
     p.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="first run a plain device copy of this many MiB (reference for HBM counters)")
-    p.add_argument("--workload", choices=("c2", "c3", "c4", "c5"), default="c2",
-                   help="c2: the headline decode layer (default); c3: ragged batched decode; "
-                        "c4: chunked prefill on the matrix cores; c5: 60-layer scoring sweep")
+    p.add_argument("--workload", choices=("c2", "c2-cached", "c3", "c4", "c5"), default="c2",
+                   help="c2: the headline decode layer (default); c2-cached: C2 with the scoring hoisted to "
+                        "cache-write time; c3: ragged batched decode; c4: chunked prefill on the matrix cores; "
+                        "c5: 60-layer scoring sweep")
     return p.parse_args()
 
 
@@ -137,7 +138,7 @@ def main():
     print(f"bench: lib {_native.LIB_PATH}", file=sys.stderr, flush=True)
 
     if args.workload != "c2":
-        {"c3": run_c3, "c4": run_c4, "c5": run_c5}[args.workload](args, torch, dev)
+        {"c2-cached": run_c2_cached, "c3": run_c3, "c4": run_c4, "c5": run_c5}[args.workload](args, torch, dev)
         return
 
     if args.copy_probe_mib:
@@ -300,6 +301,41 @@ def _per_segment_thresholds(torch, tm, z, cu_blocks, evicts):
         zmaxs.append(zm)
     dev = tm.device
     return (torch.tensor(taus, dtype=torch.float32, device=dev), torch.tensor(zmaxs, dtype=torch.float32, device=dev))
+
+
+def run_c2_cached(args, torch, dev):
+    """C2 with the scoring hoisted to cache-write time (the reference's
+    docs/mathematical_framework.md:242-250): per step, bounds from the cached
+    (dc, E_AC) of every block, the two-gate mask on the cached zeta,
+    compaction and attention.  Also times the write-time cost: the statistics
+    of one newly filled block (once per 512 decode steps)."""
+    import orthocache_amd as oc
+    from orthocache_amd import _ops, workloads
+
+    wl = workloads.c2(dev, seq=args.seq)
+    sc = _ops.score(wl.k, wl.q)
+    tau, zmax = workloads.calibrate_unified(sc.tau_max[0], sc.zeta, args.evict)
+    st = oc.block_stats(wl.k)
+    layer = oc.CachedDecodeLayer(wl.q, wl.k, wl.v, st, tau, zmax)
+    for _ in range(args.warmup):
+        layer.run()
+    torch.cuda.synchronize()
+    num_active = int(layer.num_active[0].item())
+    us = event_time_us(layer.run, args.steps, torch)
+    s, hkv, d = wl.k.shape
+    nb = s // 512
+    us_block = event_time_us(lambda: st.update(wl.k, nb - 1, 1), args.kernel_reps, torch)
+    stats_bytes = nb * hkv * (d + 2) * 4
+    q_bytes = wl.q.numel() * wl.q.element_size()
+    attend_bytes = num_active * 512 * hkv * d * 2 * 2 + q_bytes + wl.q.numel() * 2
+    step_bytes = stats_bytes + q_bytes + nb * hkv * 8 + attend_bytes
+    gbs = step_bytes / (us * 1e-6) / 1e9
+    print(json.dumps(_line("us per decode step bounds(cached stats)+compact+attend, C2 64K tok, 90% evict", us, args,
+                           {"workload": wl.name + "_cached_stats", "batch": 1, "q_heads": 32, "kv_heads": hkv,
+                            "head_dim": d, "seq_len": s, "blocks": nb, "evict": args.evict,
+                            "num_active": num_active},
+                           {"algorithmic_bytes": step_bytes, "step_gbps": round(gbs, 1),
+                            "write_time_us_per_new_block": round(us_block, 2)})), flush=True)
 
 
 def run_c3(args, torch, dev):

@@ -261,6 +261,30 @@ typedef struct oc_layer_args {
 size_t oc_decode_layer_workspace_size(const oc_layer_args* a);
 int oc_decode_layer(const oc_layer_args* a, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------- write-time block statistics
+ * The decode step with the scoring hoisted to cache-write time
+ * (docs/mathematical_framework.md:242-250, docs/technical_report.md:74: zeta
+ * is query-independent and computed once when a block enters the KV cache).
+ * When blocks are written, oc_score_blocks without queries (keys and outputs
+ * offset to the first new block) yields their statistics: dc (FWHT
+ * coefficient 0 per column, kbar = dc / sqrt(512)), e_ac and zeta.  A decode
+ * step then reads those instead of the keys: the bound
+ * tau_j(q) = q.kbar/sqrt(d) + ||q|| sqrt(E_AC)/sqrt(d) per (block, kv head)
+ * (spectral_energy.py:141-177), the two-gate mask on the cached zeta, the
+ * compaction and the attention -- the same results as oc_decode_layer on the
+ * same keys, up to fp32 rounding of the bound.  `zeta` in oc_layer_args is
+ * not written.  head_dim 64, 128, 256 or 512.  No counterpart entry point in
+ * the reference (it recomputes the FWHT on every call, pipeline.py:96-145).
+ * workspace >= oc_decode_layer_cached_workspace_size(...). */
+typedef struct oc_block_stats {
+  const float* dc;     /* (total_blocks, Hkv, head_dim) */
+  const float* e_ac;   /* (total_blocks, Hkv) */
+  const float* zeta;   /* (total_blocks, Hkv) */
+} oc_block_stats;
+size_t oc_decode_layer_cached_workspace_size(const oc_layer_args* a);
+int oc_decode_layer_cached(const oc_layer_args* a, const oc_block_stats* stats, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

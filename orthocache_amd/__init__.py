@@ -37,6 +37,7 @@ from .pipeline import orthocache_forward
 from .indirect_attention import indirect_attention, indirect_attention_fori
 from .adaptive_attention import adaptive_sparse_attention, orthocache_attention, orthocache_attention_batched
 from .varlen import mask_compact_varlen, orthocache_decode_varlen, score_varlen
+from .hoisted import BlockStats, CachedDecodeLayer, block_stats
 
 __all__ = [
     "fwht_512",
@@ -50,4 +51,5 @@ __all__ = [
     "indirect_attention", "indirect_attention_fori",
     "adaptive_sparse_attention", "orthocache_attention", "orthocache_attention_batched",
     "score_varlen", "mask_compact_varlen", "orthocache_decode_varlen",
+    "BlockStats", "block_stats", "CachedDecodeLayer",
 ]

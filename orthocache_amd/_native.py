@@ -87,11 +87,16 @@ class LayerArgs(C.Structure):
                 ("tau_max", _vp), ("zeta", _vp), ("mask", _vp), ("indices", _vp), ("num_active", _vp)]
 
 
+class BlockStats(C.Structure):
+    _fields_ = [("dc", _vp), ("e_ac", _vp), ("zeta", _vp)]
+
+
 EXPORTED_SYMBOLS = (
     "oc_last_error", "oc_abi_version", "oc_fwht512", "oc_band_energy", "oc_block_energy",
     "oc_score_blocks", "oc_query_bounds", "oc_query_bound_tiles", "oc_mask_compact",
     "oc_copy_blocks", "oc_attend_workspace_size", "oc_attend", "oc_attend_plan",
     "oc_decode_layer_workspace_size", "oc_decode_layer",
+    "oc_decode_layer_cached_workspace_size", "oc_decode_layer_cached",
 )
 
 _lib = None
@@ -130,6 +135,10 @@ def lib() -> C.CDLL:
     L.oc_attend_workspace_size.restype = C.c_size_t
     L.oc_decode_layer_workspace_size.argtypes = [C.POINTER(LayerArgs)]
     L.oc_decode_layer_workspace_size.restype = C.c_size_t
+    L.oc_decode_layer_cached_workspace_size.argtypes = [C.POINTER(LayerArgs)]
+    L.oc_decode_layer_cached_workspace_size.restype = C.c_size_t
+    L.oc_decode_layer_cached.argtypes = [C.POINTER(LayerArgs), C.POINTER(BlockStats), _vp, C.c_size_t, _vp]
+    L.oc_decode_layer_cached.restype = C.c_int
     _lib = L
     return L
 

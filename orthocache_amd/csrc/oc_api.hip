@@ -309,14 +309,26 @@ size_t oc_decode_layer_workspace_size(const oc_layer_args* a) {
   return layer_ws_layout(a, attend_ws(p)).total;
 }
 
-int oc_decode_layer(const oc_layer_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// The layer body shared by oc_decode_layer (scores from the keys) and
+// oc_decode_layer_cached (bounds from write-time block statistics).
+int decode_layer_impl(const oc_layer_args* a, const oc_block_stats* st, void* workspace, size_t workspace_bytes,
+                      void* stream, const char* name) {
   if (!a) return fail(OC_ERR_INVALID_ARGUMENT, "args is NULL");
   oc_attend_args t = layer_attend_args(a);
   oc::AttendParams ap;
   int rc = make_attend_params(&t, ap);
   if (rc) return rc;
-  if (!oc::score_supported(a->kv_dtype, a->head_dim))
+  if (st) {
+    if (!st->dc || !st->e_ac || !st->zeta) return fail(OC_ERR_INVALID_ARGUMENT, "%s: NULL block statistics", name);
+    if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256 && a->head_dim != 512)
+      return fail(OC_ERR_UNSUPPORTED, "%s: head_dim %d unsupported (64, 128, 256 or 512)", name, a->head_dim);
+  } else if (!oc::score_supported(a->kv_dtype, a->head_dim)) {
     return fail(OC_ERR_UNSUPPORTED, "scores: head_dim %d unsupported", a->head_dim);
+  }
   if (a->q_dtype != a->kv_dtype && a->q_dtype != OC_F32)
     return fail(OC_ERR_UNSUPPORTED, "q dtype must equal the kv dtype or be fp32");
   if (a->sq * a->group > 16)
@@ -328,27 +340,42 @@ int oc_decode_layer(const oc_layer_args* a, void* workspace, size_t workspace_by
     return fail(OC_ERR_WORKSPACE, "workspace %zu bytes < %zu needed", workspace_bytes, w.total);
   char* ws = static_cast<char*>(workspace);
   float* tau_max = a->tau_max ? a->tau_max : reinterpret_cast<float*>(ws + w.tau);
-  float* zeta = a->zeta ? a->zeta : reinterpret_cast<float*>(ws + w.zeta);
+  const float* zeta_in;
   int32_t* idx = a->indices ? a->indices : reinterpret_cast<int32_t*>(ws + w.idx);
   int32_t* cnt = a->num_active ? a->num_active : reinterpret_cast<int32_t*>(ws + w.cnt);
   const hipStream_t s = (hipStream_t)stream;
 
-  // 1. Scores.
-  oc::ScoreParams sp{};
-  sp.k = a->k; sp.k_tok_stride = a->k_tok_stride; sp.k_head_stride = a->k_head_stride; sp.k_dtype = a->kv_dtype;
-  sp.head_dim = a->head_dim; sp.num_kv_heads = a->num_kv_heads; sp.total_blocks = a->total_blocks;
-  sp.cu_blocks = a->cu_blocks; sp.num_segments = nseg;
-  sp.q = a->q; sp.q_dtype = a->q_dtype;
-  sp.q_seg_stride = a->q_seg_stride; sp.q_tok_stride = a->q_tok_stride; sp.q_head_stride = a->q_head_stride;
-  sp.sq = a->sq; sp.group = a->group;
-  sp.tau_max = tau_max; sp.zeta = zeta;
-  rc = hip_check(oc::launch_score(sp, s), "oc_decode_layer scores");
-  if (rc) return rc;
+  // 1. Scores: from the keys, or bounds from the cached statistics.
+  if (st) {
+    oc::CachedBoundParams cp{};
+    cp.dc = st->dc; cp.e_ac = st->e_ac;
+    cp.q = a->q; cp.q_dtype = a->q_dtype;
+    cp.q_seg_stride = a->q_seg_stride; cp.q_tok_stride = a->q_tok_stride; cp.q_head_stride = a->q_head_stride;
+    cp.sq = a->sq; cp.group = a->group; cp.head_dim = a->head_dim; cp.num_kv_heads = a->num_kv_heads;
+    cp.total_blocks = a->total_blocks; cp.cu_blocks = a->cu_blocks; cp.num_segments = nseg;
+    cp.tau_max = tau_max;
+    rc = hip_check(oc::launch_cached_bound(cp, s), "oc_decode_layer_cached bounds");
+    if (rc) return rc;
+    zeta_in = st->zeta;
+  } else {
+    float* zeta = a->zeta ? a->zeta : reinterpret_cast<float*>(ws + w.zeta);
+    oc::ScoreParams sp{};
+    sp.k = a->k; sp.k_tok_stride = a->k_tok_stride; sp.k_head_stride = a->k_head_stride; sp.k_dtype = a->kv_dtype;
+    sp.head_dim = a->head_dim; sp.num_kv_heads = a->num_kv_heads; sp.total_blocks = a->total_blocks;
+    sp.cu_blocks = a->cu_blocks; sp.num_segments = nseg;
+    sp.q = a->q; sp.q_dtype = a->q_dtype;
+    sp.q_seg_stride = a->q_seg_stride; sp.q_tok_stride = a->q_tok_stride; sp.q_head_stride = a->q_head_stride;
+    sp.sq = a->sq; sp.group = a->group;
+    sp.tau_max = tau_max; sp.zeta = zeta;
+    rc = hip_check(oc::launch_score(sp, s), "oc_decode_layer scores");
+    if (rc) return rc;
+    zeta_in = zeta;
+  }
 
   // 2. Mask + compaction.
   {
     oc::CompactParams cp{};
-    cp.tau_max = tau_max; cp.tau_parts = 1; cp.zeta = zeta;
+    cp.tau_max = tau_max; cp.tau_parts = 1; cp.zeta = zeta_in;
     cp.tau_arr = a->tau_arr; cp.tau = a->tau; cp.zmax_arr = a->zeta_max_arr; cp.zeta_max = a->zeta_max;
     cp.cu_blocks = a->cu_blocks; cp.num_segments = nseg; cp.nb_single = a->total_blocks;
     cp.num_kv_heads = a->num_kv_heads; cp.total_blocks = a->total_blocks;
@@ -361,7 +388,23 @@ int oc_decode_layer(const oc_layer_args* a, void* workspace, size_t workspace_by
   ap.indices = idx;
   ap.counts = cnt;
   attend_bind_ws(ap, ws + w.attend);
-  return hip_check(oc::launch_attend(ap, s), "oc_decode_layer attend");
+  return hip_check(oc::launch_attend(ap, s), name);
+}
+
+}  // namespace
+
+extern "C" {
+
+int oc_decode_layer(const oc_layer_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  return decode_layer_impl(a, nullptr, workspace, workspace_bytes, stream, "oc_decode_layer");
+}
+
+size_t oc_decode_layer_cached_workspace_size(const oc_layer_args* a) { return oc_decode_layer_workspace_size(a); }
+
+int oc_decode_layer_cached(const oc_layer_args* a, const oc_block_stats* stats, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  if (!stats) return fail(OC_ERR_INVALID_ARGUMENT, "stats is NULL");
+  return decode_layer_impl(a, stats, workspace, workspace_bytes, stream, "oc_decode_layer_cached");
 }
 
 }  // extern "C"

@@ -38,7 +38,22 @@ struct BoundParams {
   int64_t q_tok_stride, q_head_stride;
   int sq, group, head_dim, num_kv_heads, num_blocks;
   float* bounds;       // (sq*group, nb, Hkv) or null
-  float* tau_part;     // (ceil(sq*group/32), nb, Hkv) or null
+  float* tau_part;     // (ceil(sq*group/64), nb, Hkv) or null
+};
+
+// Bound from write-time block statistics (dc, E_AC of oc_score_blocks), for
+// few queries per kv head: tau_max[j, h] = NaN-propagating max over the
+// segment's query rows.
+struct CachedBoundParams {
+  const float* dc;     // (total_blocks, Hkv, D)
+  const float* e_ac;   // (total_blocks, Hkv)
+  const void* q;
+  int q_dtype;
+  int64_t q_seg_stride, q_tok_stride, q_head_stride;
+  int sq, group, head_dim, num_kv_heads, total_blocks;
+  const int* cu_blocks;  // (num_segments + 1) or null
+  int num_segments;
+  float* tau_max;      // (total_blocks, Hkv)
 };
 
 struct EnergyParams {
@@ -49,6 +64,7 @@ struct EnergyParams {
   float* out;
 };
 
+hipError_t launch_cached_bound(const CachedBoundParams& p, hipStream_t s);
 int bound_query_tile();  // queries per partial maximum of the bound kernel
 int bound_block_tile();
 hipError_t launch_bound(const BoundParams& p, hipStream_t s);

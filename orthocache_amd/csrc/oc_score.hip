@@ -361,6 +361,84 @@ __global__ __launch_bounds__(256) void bound_kernel(BoundParams p) {
   }
 }
 
+// Query-aware bound from write-time block statistics: with kbar, E_AC and
+// zeta computed once when a block enters the cache (oc_score_blocks without
+// queries), a decode step only needs tau_j(q) = q.kbar/sqrt(d) +
+// ||q|| sqrt(E_AC)/sqrt(d) per (block, kv head), max over the query rows
+// sharing the kv head -- the hoisting of docs/mathematical_framework.md:242-250.
+// One wave per (block, kv head) tile: lane l holds dims l*DPL .. +DPL of dc
+// (kbar = dc / sqrt(512), as the scoring kernel forms it) and of each query;
+// dot products and squared norms are wave sums.  Reads Hkv*D*4 B per block
+// instead of the block's keys.
+template <int QDT, int DPL>
+__global__ __launch_bounds__(256) void cached_bound_kernel(CachedBoundParams p) {
+  using EQ = Elt<QDT>;
+  constexpr int D = DPL * kWave;
+  const int H = p.num_kv_heads;
+  const int tile = blockIdx.x * (256 / kWave) + (int)(threadIdx.x / kWave);
+  if (tile >= p.total_blocks * H) return;  // whole waves exit together
+  const int lane = threadIdx.x & (kWave - 1);
+  const int gb = tile / H, h = tile - gb * H;
+  int seg = 0;
+  if (p.cu_blocks) {
+    int lo = 0, hi = p.num_segments - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (p.cu_blocks[mid] <= gb) lo = mid; else hi = mid - 1;
+    }
+    seg = lo;
+  }
+  float kb[DPL];
+  const float* dcp = p.dc + (int64_t)tile * D + lane * DPL;
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) kb[j] = dcp[j] / kSqrt512;  // spectral_energy.py:166
+  const float sqrt_d = sqrtf((float)D);
+  const float sqrt_eac = sqrtf(p.e_ac[tile]);
+  const int nq = p.sq * p.group;
+  float best = -INFINITY;
+  for (int qi = 0; qi < nq; ++qi) {
+    const int st = qi / p.group, g = qi - st * p.group;
+    const int64_t qoff = (int64_t)seg * p.q_seg_stride + (int64_t)st * p.q_tok_stride +
+                         (int64_t)(h * p.group + g) * p.q_head_stride + lane * DPL;
+    float a = 0.f, b = 0.f;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      const float v = EQ::load1(p.q, qoff + j);
+      a = fmaf(v, kb[j], a);
+      b = fmaf(v, v, b);
+    }
+    a = wave_sum(a);
+    b = wave_sum(b);
+    const float align = a / sqrt_d;
+    const float resid = (sqrtf(b) * sqrt_eac) / sqrt_d;
+    best = nanmax(align + resid, best);
+  }
+  if (lane == 0) p.tau_max[tile] = best;
+}
+
+template <int QDT>
+static hipError_t launch_cached_bound_q(const CachedBoundParams& p, hipStream_t s) {
+  const dim3 grid((unsigned)(((int64_t)p.total_blocks * p.num_kv_heads + 3) / 4));
+  switch (p.head_dim) {
+    case 64: hipLaunchKernelGGL((cached_bound_kernel<QDT, 1>), grid, dim3(256), 0, s, p); break;
+    case 128: hipLaunchKernelGGL((cached_bound_kernel<QDT, 2>), grid, dim3(256), 0, s, p); break;
+    case 256: hipLaunchKernelGGL((cached_bound_kernel<QDT, 4>), grid, dim3(256), 0, s, p); break;
+    case 512: hipLaunchKernelGGL((cached_bound_kernel<QDT, 8>), grid, dim3(256), 0, s, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_cached_bound(const CachedBoundParams& p, hipStream_t s) {
+  if ((int64_t)p.total_blocks * p.num_kv_heads == 0) return hipSuccess;
+  switch (p.q_dtype) {
+    case kF32: return launch_cached_bound_q<kF32>(p, s);
+    case kBF16: return launch_cached_bound_q<kBF16>(p, s);
+    case kF16: return launch_cached_bound_q<kF16>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 // Spatial energy sum k^2 per (block, head) for any block size
 // (spectral_energy.py:21-35).  One workgroup per (block, head).
 __global__ __launch_bounds__(256) void block_energy_kernel(EnergyParams p) {

@@ -58,7 +58,8 @@ def test_struct_sizes_match_header_layout(lib):
     text = open(HEADER).read()
     for cname, py in (("oc_fwht_args", N.FwhtArgs), ("oc_score_args", N.ScoreArgs),
                       ("oc_bound_args", N.BoundArgs), ("oc_compact_args", N.CompactArgs),
-                      ("oc_attend_args", N.AttendArgs), ("oc_layer_args", N.LayerArgs)):
+                      ("oc_attend_args", N.AttendArgs), ("oc_layer_args", N.LayerArgs),
+                      ("oc_block_stats", N.BlockStats)):
         body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (cname, cname), text, re.S).group(1)
         body = re.sub(r"/\*.*?\*/", "", body)
         names = []
@@ -92,6 +93,16 @@ def test_validation_errors_without_gpu(lib):
     assert lib.oc_query_bound_tiles(2, 16) == 1
     assert lib.oc_query_bound_tiles(512, 1) == 8
     assert lib.oc_query_bound_tiles(65, 1) == 2
+
+
+def test_cached_layer_rejects_null_stats(lib):
+    from orthocache_amd import _native as N
+
+    a = N.LayerArgs()
+    assert lib.oc_decode_layer_cached(C.byref(a), None, None, 0, None) == -1
+    st = N.BlockStats()
+    assert lib.oc_decode_layer_cached(C.byref(a), C.byref(st), None, 0, None) == -1
+    assert lib.oc_decode_layer_cached_workspace_size(C.byref(a)) == 0
 
 
 def test_attend_workspace_rejects_bad_args(lib):
