@@ -20,6 +20,15 @@
  *    workspaces are caller-owned.  Counts such as num_active stay on device.
  *  - Return 0 on success or a negative OC_ERR_* code; oc_last_error() gives
  *    a message (thread-local).  Entry points are stateless and reentrant.
+ *  - Paged caches: the argument structs of scoring, attention and the layer
+ *    take `pages`, an int32 device array (total_blocks): the block with
+ *    flattened index j (segment offsets included) lives in physical page
+ *    pages[j] of the key/value pool, i.e. at token pages[j] * block_size.
+ *    NULL means block j is at token j * block_size (contiguous cache).  Masks,
+ *    scores and block lists stay in logical block numbering.  num_pages is the
+ *    pool size in pages; page numbers outside [0, num_pages) are clamped into
+ *    it (the kernels never read outside the pool), as are block-list entries
+ *    outside their segment.  (ABI version 2 appended these fields.)
  */
 #ifndef ORTHOCACHE_HIP_H
 #define ORTHOCACHE_HIP_H
@@ -31,7 +40,7 @@
 extern "C" {
 #endif
 
-#define OC_ABI_VERSION 1
+#define OC_ABI_VERSION 2
 
 #define OC_OK 0
 #define OC_ERR_INVALID_ARGUMENT (-1)
@@ -111,6 +120,8 @@ typedef struct oc_score_args {
   float* e_mid;
   float* e_high;
   float* e_ac;
+  const int32_t* pages; /* (total_blocks) physical page per block, or NULL */
+  int32_t num_pages;    /* pages in the key pool (used when pages != NULL) */
 } oc_score_args;
 int oc_score_blocks(const oc_score_args* a, void* stream);
 
@@ -211,6 +222,8 @@ typedef struct oc_attend_args {
   void* out;
   int32_t out_dtype;
   int64_t out_seg_stride, out_tok_stride, out_head_stride;
+  const int32_t* pages;    /* (total_blocks) physical page per block, or NULL */
+  int32_t num_pages;       /* pages in the key/value pools (used when pages != NULL) */
 } oc_attend_args;
 size_t oc_attend_workspace_size(const oc_attend_args* a);
 int oc_attend(const oc_attend_args* a, void* workspace, size_t workspace_bytes, void* stream);
@@ -257,6 +270,8 @@ typedef struct oc_layer_args {
   uint8_t* mask;
   int32_t* indices;
   int32_t* num_active;
+  const int32_t* pages;    /* (total_blocks) physical page per block, or NULL */
+  int32_t num_pages;       /* pages in the key/value pools (used when pages != NULL) */
 } oc_layer_args;
 size_t oc_decode_layer_workspace_size(const oc_layer_args* a);
 int oc_decode_layer(const oc_layer_args* a, void* workspace, size_t workspace_bytes, void* stream);

@@ -38,6 +38,7 @@ from .indirect_attention import indirect_attention, indirect_attention_fori
 from .adaptive_attention import adaptive_sparse_attention, orthocache_attention, orthocache_attention_batched
 from .varlen import mask_compact_varlen, orthocache_decode_varlen, score_varlen
 from .hoisted import BlockStats, CachedDecodeLayer, block_stats
+from .paged import flatten_block_table, orthocache_decode_paged
 
 __all__ = [
     "fwht_512",
@@ -52,4 +53,5 @@ __all__ = [
     "adaptive_sparse_attention", "orthocache_attention", "orthocache_attention_batched",
     "score_varlen", "mask_compact_varlen", "orthocache_decode_varlen",
     "BlockStats", "block_stats", "CachedDecodeLayer",
+    "flatten_block_table", "orthocache_decode_paged",
 ]

@@ -97,7 +97,7 @@ INLINE_QUERY_LIMIT = 16
 
 def score(keys: torch.Tensor, q: torch.Tensor | None = None, *, want_bands: bool = False,
           want_bounds: bool = False, want_zeta: bool = True, cu_blocks: torch.Tensor | None = None,
-          num_segments: int = 1) -> Scores:
+          num_segments: int = 1, pages: torch.Tensor | None = None) -> Scores:
     """One pass over the keys: zeta, bands and (with q) the query-aware bound.
 
     keys: (S, Hkv, D), S a multiple of 512.  q: (Sq, Hq, D) for one segment or
@@ -111,6 +111,9 @@ def score(keys: torch.Tensor, q: torch.Tensor | None = None, *, want_bands: bool
     if s % BLOCK:
         raise ValueError(f"seq_len {s} is not a multiple of the block size {BLOCK}")
     nb = s // BLOCK
+    pages = _pages_view(pages, keys)
+    if pages is not None:
+        nb = pages.shape[0]  # logical blocks; keys is the page pool
     dev = keys.device
     f32 = dict(dtype=torch.float32, device=dev)
     tiles = (nb, hkv)
@@ -150,6 +153,8 @@ def score(keys: torch.Tensor, q: torch.Tensor | None = None, *, want_bands: bool
     a.keys_tok_stride = keys.stride(0); a.keys_head_stride = keys.stride(1)
     a.head_dim = d; a.num_kv_heads = hkv; a.total_blocks = nb
     a.cu_blocks = ptr(cu_blocks); a.num_segments = num_segments
+    a.pages = ptr(pages)
+    a.num_pages = s // BLOCK
     if inline:
         a.q = ptr(q); a.q_dtype = dtype_code(q.dtype)
         a.q_seg_stride = q.stride(0) if cu_blocks is not None else 0
@@ -170,6 +175,20 @@ def score(keys: torch.Tensor, q: torch.Tensor | None = None, *, want_bands: bool
                         sq, group, d, hkv, nb, ptr(res.bounds), ptr(res.tau_max))
         check(lib().oc_query_bounds(C.byref(b), stream_ptr(dev)), "oc_query_bounds")
     return res
+
+
+def _pages_view(pages, pool: torch.Tensor, block_size: int = BLOCK):
+    """Validate a page list (int32, one physical page of ``pool`` per logical
+    block) or pass None through."""
+    if pages is None:
+        return None
+    if not isinstance(pages, torch.Tensor) or pages.dim() != 1 or pages.dtype != torch.int32:
+        raise ValueError("pages must be a 1-D int32 tensor (one physical page per logical block)")
+    if pages.device != pool.device:
+        raise ValueError("pages must be on the keys' device")
+    if pool.shape[0] % block_size:
+        raise ValueError(f"the page pool's token count {pool.shape[0]} is not a multiple of {block_size}")
+    return pages.contiguous()
 
 
 # ------------------------------------------------------ mask + compaction
@@ -269,11 +288,12 @@ def copy_blocks(src: torch.Tensor, dst: torch.Tensor, indices: torch.Tensor, num
 def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, indices: torch.Tensor, counts: torch.Tensor, *,
            block_size: int = BLOCK, per_head: bool = False, uniform: torch.Tensor | None = None,
            out_dtype: torch.dtype | None = None, cu_blocks: torch.Tensor | None = None,
-           num_segments: int = 1, out: torch.Tensor | None = None) -> torch.Tensor:
+           num_segments: int = 1, out: torch.Tensor | None = None, pages: torch.Tensor | None = None) -> torch.Tensor:
     """Attention over the listed blocks.  q: (Sq, Hq, D) (or (B, Sq, Hq, D) with
     cu_blocks); k, v: (S, Hkv, D).  Returns q-shaped output in out_dtype."""
     a, out, q = _attend_args(q, k, v, indices, counts, block_size=block_size, per_head=per_head, uniform=uniform,
-                             out_dtype=out_dtype, cu_blocks=cu_blocks, num_segments=num_segments, out=out)
+                             out_dtype=out_dtype, cu_blocks=cu_blocks, num_segments=num_segments, out=out,
+                             pages=pages)
     L = lib()
     ws_bytes = int(L.oc_attend_workspace_size(C.byref(a)))
     if ws_bytes == 0 and a.total_blocks > 0:
@@ -295,7 +315,7 @@ def attend_plan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, indices: torc
 
 
 def _attend_args(q, k, v, indices, counts, *, block_size: int = BLOCK, per_head: bool = False,
-                 uniform=None, out_dtype=None, cu_blocks=None, num_segments: int = 1, out=None):
+                 uniform=None, out_dtype=None, cu_blocks=None, num_segments: int = 1, out=None, pages=None):
     require_gpu(q, k, v, indices, counts)
     out_dtype = out_dtype or q.dtype
     k = _kv_view(k, "keys")
@@ -323,6 +343,11 @@ def _attend_args(q, k, v, indices, counts, *, block_size: int = BLOCK, per_head:
     a.v_tok_stride = v.stride(0); a.v_head_stride = v.stride(1)
     a.head_dim = d; a.num_kv_heads = hkv; a.group = group; a.sq = sq
     a.block_size = block_size; a.total_blocks = s // block_size
+    pages = _pages_view(pages, k, block_size)
+    if pages is not None:
+        a.total_blocks = pages.shape[0]
+        a.pages = ptr(pages)
+        a.num_pages = s // block_size
     a.cu_blocks = ptr(cu_blocks); a.num_segments = num_segments
     a.indices = ptr(indices); a.counts = ptr(counts); a.per_head = 1 if per_head else 0
     a.uniform = ptr(uniform)
@@ -342,8 +367,8 @@ class DecodeLayer:
     """
 
     def __init__(self, q, k, v, tau, zeta_max, *, cu_blocks=None, num_segments=1, out=None,
-                 out_dtype=None, keep_scores=True):
-        require_gpu(q, k, v, cu_blocks)
+                 out_dtype=None, keep_scores=True, pages=None):
+        require_gpu(q, k, v, cu_blocks, pages)
         self.k = _kv_view(k, "keys")
         self.v = _kv_view(v, "values")
         self.q = _q_view(q, self.k.dtype)
@@ -351,6 +376,9 @@ class DecodeLayer:
         if s % BLOCK:
             raise ValueError(f"seq_len {s} is not a multiple of {BLOCK}")
         nb = s // BLOCK
+        self.pages = _pages_view(pages, self.k)
+        if self.pages is not None:
+            nb = self.pages.shape[0]
         dev = self.k.device
         self.device = dev
         group = kv_group(self.q.shape[-2], hkv)
@@ -370,6 +398,8 @@ class DecodeLayer:
         a.v_tok_stride = self.v.stride(0); a.v_head_stride = self.v.stride(1)
         a.head_dim = d; a.num_kv_heads = hkv; a.group = group; a.sq = q_.shape[-3]
         a.total_blocks = nb; a.cu_blocks = ptr(cu_blocks); a.num_segments = num_segments
+        a.pages = ptr(self.pages)
+        a.num_pages = s // BLOCK
         self._tau_t = self._zmax_t = None
         if isinstance(tau, torch.Tensor):
             self._tau_t = tau.to(device=dev, dtype=torch.float32).contiguous()
@@ -415,7 +445,7 @@ class DecodeLayer:
         sa.total_blocks = a.total_blocks; sa.cu_blocks = a.cu_blocks; sa.num_segments = a.num_segments
         sa.q = a.q; sa.q_dtype = a.q_dtype; sa.q_seg_stride = a.q_seg_stride; sa.q_tok_stride = a.q_tok_stride
         sa.q_head_stride = a.q_head_stride; sa.sq = a.sq; sa.group = a.group
-        sa.tau_max = a.tau_max; sa.zeta = a.zeta
+        sa.tau_max = a.tau_max; sa.zeta = a.zeta; sa.pages = a.pages; sa.num_pages = a.num_pages
         ca = N.CompactArgs()
         ca.tau_max = a.tau_max; ca.tau_parts = 1; ca.zeta = a.zeta
         ca.tau_arr = a.tau_arr; ca.tau = a.tau; ca.zeta_max_arr = a.zeta_max_arr; ca.zeta_max = a.zeta_max
@@ -426,7 +456,7 @@ class DecodeLayer:
         for f in ("q", "q_dtype", "q_seg_stride", "q_tok_stride", "q_head_stride", "k", "v", "kv_dtype",
                   "k_tok_stride", "k_head_stride", "v_tok_stride", "v_head_stride", "head_dim", "num_kv_heads",
                   "group", "sq", "total_blocks", "cu_blocks", "num_segments", "out", "out_dtype",
-                  "out_seg_stride", "out_tok_stride", "out_head_stride"):
+                  "out_seg_stride", "out_tok_stride", "out_head_stride", "pages", "num_pages"):
             setattr(ta, f, getattr(a, f))
         ta.block_size = BLOCK; ta.indices = a.indices; ta.counts = a.num_active
         ws = int(L.oc_attend_workspace_size(C.byref(ta)))

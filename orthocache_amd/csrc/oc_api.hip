@@ -99,10 +99,12 @@ int oc_score_blocks(const oc_score_args* a, void* stream) {
     if (a->cu_blocks && a->num_segments > 4096)
       return fail(OC_ERR_UNSUPPORTED, "at most 4096 segments per call");
   }
+  if (a->pages && a->num_pages <= 0) return fail(OC_ERR_INVALID_ARGUMENT, "pages given with num_pages %d", a->num_pages);
   oc::ScoreParams p{a->keys, a->keys_tok_stride, a->keys_head_stride, a->keys_dtype, a->head_dim,
                     a->num_kv_heads, a->total_blocks, a->cu_blocks, a->cu_blocks ? a->num_segments : 1,
                     a->q, a->q_dtype, a->q_seg_stride, a->q_tok_stride, a->q_head_stride, a->sq, a->group,
-                    a->tau_max, a->zeta, a->dc, a->e_low, a->e_mid, a->e_high, a->e_ac};
+                    a->tau_max, a->zeta, a->dc, a->e_low, a->e_mid, a->e_high, a->e_ac, a->pages,
+                    a->num_pages};
   return hip_check(oc::launch_score(p, (hipStream_t)stream), "oc_score_blocks");
 }
 
@@ -182,6 +184,7 @@ int make_attend_params(const oc_attend_args* a, oc::AttendParams& p) {
   if ((int64_t)nseg * a->num_kv_heads > oc::kMaxLists)
     return fail(OC_ERR_UNSUPPORTED, "segments x kv heads = %lld exceeds %d", (long long)nseg * a->num_kv_heads, oc::kMaxLists);
   if (!a->indices || !a->counts) return fail(OC_ERR_INVALID_ARGUMENT, "indices/counts are NULL");
+  if (a->pages && a->num_pages <= 0) return fail(OC_ERR_INVALID_ARGUMENT, "pages given with num_pages %d", a->num_pages);
   const int chunk = oc::attend_chunk(a->kv_dtype, a->head_dim, a->sq * a->group);
   p = oc::AttendParams{};
   p.q = a->q; p.q_dtype = a->q_dtype;
@@ -198,6 +201,7 @@ int make_attend_params(const oc_attend_args* a, oc::AttendParams& p) {
   p.part_o = nullptr; p.part_ml = nullptr;
   p.out = a->out; p.out_dtype = a->out_dtype;
   p.out_seg_stride = a->out_seg_stride; p.out_tok_stride = a->out_tok_stride; p.out_head_stride = a->out_head_stride;
+  p.pages = a->pages; p.num_pages = a->num_pages;
   p.prefill = oc::prefill_supported(a->kv_dtype, a->q_dtype, a->head_dim, a->sq * a->group, a->block_size) ? 1 : 0;
   // The prefill kernel keeps per-thread offsets inside a 64-token tile in 32 bits.
   if (a->k_tok_stride >= (1 << 24) || a->v_tok_stride >= (1 << 24)) p.prefill = 0;
@@ -294,6 +298,7 @@ oc_attend_args layer_attend_args(const oc_layer_args* a) {
   t.per_head = 0; t.uniform = nullptr;
   t.out = a->out; t.out_dtype = a->out_dtype;
   t.out_seg_stride = a->out_seg_stride; t.out_tok_stride = a->out_tok_stride; t.out_head_stride = a->out_head_stride;
+  t.pages = a->pages; t.num_pages = a->num_pages;
   return t;
 }
 
@@ -367,6 +372,7 @@ int decode_layer_impl(const oc_layer_args* a, const oc_block_stats* st, void* wo
     sp.q_seg_stride = a->q_seg_stride; sp.q_tok_stride = a->q_tok_stride; sp.q_head_stride = a->q_head_stride;
     sp.sq = a->sq; sp.group = a->group;
     sp.tau_max = tau_max; sp.zeta = zeta;
+    sp.pages = a->pages; sp.num_pages = a->num_pages;
     rc = hip_check(oc::launch_score(sp, s), "oc_decode_layer scores");
     if (rc) return rc;
     zeta_in = zeta;

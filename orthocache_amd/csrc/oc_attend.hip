@@ -37,9 +37,17 @@
 
 namespace oc {
 
+// Blocks of segment `seg`.
+__device__ __forceinline__ int segment_blocks(const AttendParams& p, int seg) {
+  return p.cu_blocks ? p.cu_blocks[seg + 1] - p.cu_blocks[seg] : p.total_blocks;
+}
+
+// Entries of a block list, clamped to [0, blocks of its segment] so that a
+// malformed count never indexes outside the list arrays.
 __device__ __forceinline__ int list_count(const AttendParams& p, int list) {
-  if (p.per_head) return p.counts[list];
-  return p.counts[list / p.num_kv_heads];
+  const int seg = list / p.num_kv_heads;
+  const int c = p.per_head ? p.counts[list] : p.counts[seg];
+  return min(max(c, 0), segment_blocks(p, seg));
 }
 
 // Exclusive scan of one int per thread over a 256-thread workgroup.
@@ -158,7 +166,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendPar
   // One segment with one list shared by the heads: every list has the same
   // length, so no prefix is needed.
   const bool uniform_lists = !p.per_head && p.num_segments == 1;
-  const int ipl = uniform_lists ? p.counts[0] * p.nchunk * nqg : 0;
+  const int ipl = uniform_lists ? min(max(p.counts[0], 0), p.total_blocks) * p.nchunk * nqg : 0;
   const int total_items = uniform_lists ? ipl * nlists : build_item_offsets(p, s_off, nqg);
 
   const int t = threadIdx.x;
@@ -184,8 +192,10 @@ __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendPar
     const int seg = list / p.num_kv_heads;
     const int h = list - seg * p.num_kv_heads;
     const int off = p.cu_blocks ? p.cu_blocks[seg] : 0;
-    const int blk = p.indices[(p.per_head ? (int64_t)h * p.total_blocks : 0) + off + i];
-    const int64_t tok0 = (int64_t)(off + blk) * p.block_size + (int64_t)c * p.chunk;
+    const int nbs = p.cu_blocks ? p.cu_blocks[seg + 1] - off : p.total_blocks;
+    const int blk = min(max(p.indices[(p.per_head ? (int64_t)h * p.total_blocks : 0) + off + i], 0), nbs - 1);
+    const int64_t page = page_of(p.pages, p.num_pages, (int64_t)off + blk);
+    const int64_t tok0 = page * p.block_size + (int64_t)c * p.chunk;
     const int nrows = min(p.chunk, p.block_size - c * p.chunk);
 
     const char* kb = reinterpret_cast<const char*>(p.k) +

@@ -133,11 +133,21 @@ struct ScoreParams {
   float* e_mid;
   float* e_high;
   float* e_ac;
+  const int* pages;  // (total_blocks) physical 512-token page of each block, or null (pages = blocks)
+  int num_pages;     // pool size in pages (page numbers are clamped into it)
 };
 
 bool score_supported(int dt, int head_dim);
 hipError_t launch_score(const ScoreParams& p, hipStream_t s);
 hipError_t launch_copy_blocks(const CopyParams& p, hipStream_t s);
+
+// Physical page of flattened block j: pages[j] clamped into [0, num_pages),
+// or j itself for a contiguous cache.
+__device__ __forceinline__ int64_t page_of(const int* pages, int num_pages, int64_t j) {
+  if (!pages) return j;
+  const int pg = pages[j];
+  return (int64_t)((unsigned)pg < (unsigned)num_pages ? pg : (pg < 0 ? 0 : num_pages - 1));
+}
 
 // ---------------------------------------------------------- oc_attend.hip
 constexpr int kQG = 8;           // queries per attention work item
@@ -168,6 +178,8 @@ struct AttendParams {
   void* out;
   int out_dtype;
   int64_t out_seg_stride, out_tok_stride, out_head_stride;
+  const int* pages;  // (total_blocks) physical page of each block (block_size tokens), or null
+  int num_pages;     // pool size in pages (page numbers are clamped into it)
 };
 
 bool attend_supported(int dt, int head_dim);

@@ -144,14 +144,17 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
   const int seg = id / p.num_kv_heads;
   const int list = seg * p.num_kv_heads + h;
 
-  const int count = p.per_head ? p.counts[list] : p.counts[seg];
+  const int off = p.cu_blocks ? p.cu_blocks[seg] : 0;
+  const int nbs = p.cu_blocks ? p.cu_blocks[seg + 1] - off : p.total_blocks;
+  // Counts and list entries are clamped into the segment, so a malformed list
+  // never addresses outside the caches.
+  const int count = min(max(p.per_head ? p.counts[list] : p.counts[seg], 0), nbs);
   const int tpb = p.block_size / kPfKeys;
   const int ntiles = count * tpb;
   const int per = (ntiles + p.nsplit - 1) / p.nsplit;
   const int t0 = min(split * per, ntiles);
   const int t1 = min(t0 + per, ntiles);
   const bool uni = (p.uniform != nullptr) && (p.uniform[list] != 0);
-  const int off = p.cu_blocks ? p.cu_blocks[seg] : 0;
   const int* idx = p.indices + (p.per_head ? (int64_t)h * p.total_blocks : 0) + off;
 
   const int t = threadIdx.x;
@@ -203,8 +206,9 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
   for (int i = 0; i < KPT; ++i) voff[i] = (int)((vk0 + i) * vrow_g) + vdch * 16;
   u32x4_t kr[KCH], vr[KPT];
   auto load_tile = [&](int tau) {
-    const int blk = idx[tau / tpb];
-    const int64_t tok0 = (int64_t)(off + blk) * p.block_size + (int64_t)(tau % tpb) * kPfKeys;
+    const int blk = min(max(idx[tau / tpb], 0), nbs - 1);
+    const int64_t page = page_of(p.pages, p.num_pages, (int64_t)off + blk);
+    const int64_t tok0 = page * p.block_size + (int64_t)(tau % tpb) * kPfKeys;
     const char* kt = kbase + tok0 * krow_g;
     const char* vt = vbase + tok0 * vrow_g;
 #pragma unroll

@@ -63,8 +63,10 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
   const int slot = t / LPR;
 
   const int64_t row_bytes = p.k_tok_stride * ESZ;
+  // Paged caches: the block's keys live in physical page pages[gb].
+  const int64_t page = page_of(p.pages, p.num_pages, gb);
   const char* base = reinterpret_cast<const char*>(p.k) +
-                     ((int64_t)gb * kBlock * p.k_tok_stride + (int64_t)h * p.k_head_stride +
+                     (page * kBlock * p.k_tok_stride + (int64_t)h * p.k_head_stride +
                       (int64_t)cc * VEC) * ESZ;
 
   // Query-aware bound inputs, requested before the key stream so their

@@ -27,7 +27,7 @@ import torch
 
 from . import _native as N
 from ._native import check, dtype_code, lib, ptr, require_gpu, stream_ptr
-from ._ops import BLOCK, DecodeLayer, _kv_view
+from ._ops import BLOCK, DecodeLayer, _kv_view, _pages_view
 
 
 @dataclass
@@ -44,13 +44,19 @@ class BlockStats:
     def num_blocks(self) -> int:
         return self.zeta.shape[0]
 
-    def update(self, keys: torch.Tensor, first_block: int, num_blocks: int | None = None) -> "BlockStats":
+    def update(self, keys: torch.Tensor, first_block: int, num_blocks: int | None = None,
+               pages: torch.Tensor | None = None) -> "BlockStats":
         """(Re)compute the statistics of blocks [first_block, first_block + num_blocks)
         of ``keys`` (S, Hkv, D) in place -- e.g. the blocks a decode step just
-        filled.  Only those blocks' keys are read."""
+        filled.  Only those blocks' keys are read.  With ``pages`` (int32, one
+        physical page of the pool ``keys`` per logical block) the blocks are
+        logical blocks of a paged cache."""
         keys = _kv_view(keys, "keys")
         s, hkv, d = keys.shape
         nb = s // BLOCK
+        pages = _pages_view(pages, keys)
+        if pages is not None:
+            nb = pages.shape[0]
         n = nb - first_block if num_blocks is None else num_blocks
         if first_block < 0 or n < 0 or first_block + n > min(nb, self.num_blocks):
             raise ValueError(f"blocks [{first_block}, {first_block + n}) outside the cache ({nb} blocks)")
@@ -60,7 +66,12 @@ class BlockStats:
             return self
         a = N.ScoreArgs()
         esz = keys.element_size()
-        a.keys = ptr(keys) + first_block * BLOCK * keys.stride(0) * esz
+        if pages is None:
+            a.keys = ptr(keys) + first_block * BLOCK * keys.stride(0) * esz
+        else:
+            a.keys = ptr(keys)
+            a.pages = ptr(pages) + first_block * 4
+            a.num_pages = s // BLOCK
         a.keys_dtype = dtype_code(keys.dtype)
         a.keys_tok_stride = keys.stride(0); a.keys_head_stride = keys.stride(1)
         a.head_dim = d; a.num_kv_heads = hkv; a.total_blocks = n; a.num_segments = 1
@@ -71,22 +82,25 @@ class BlockStats:
         return self
 
 
-def block_stats(keys: torch.Tensor, capacity_blocks: int | None = None) -> BlockStats:
+def block_stats(keys: torch.Tensor, capacity_blocks: int | None = None,
+                pages: torch.Tensor | None = None) -> BlockStats:
     """Statistics of every block of ``keys`` (S, Hkv, D), S a multiple of 512,
-    in buffers sized for ``capacity_blocks`` (default: the blocks present)."""
-    require_gpu(keys)
+    in buffers sized for ``capacity_blocks`` (default: the blocks present).
+    With ``pages``, ``keys`` is a page pool and the blocks are the logical
+    blocks the page list names."""
+    require_gpu(keys, pages)
     keys = _kv_view(keys, "keys")
     s, hkv, d = keys.shape
     if s % BLOCK:
         raise ValueError(f"seq_len {s} is not a multiple of the block size {BLOCK}")
-    nb = s // BLOCK
+    nb = s // BLOCK if pages is None else pages.shape[0]
     cap = nb if capacity_blocks is None else capacity_blocks
     if cap < nb:
         raise ValueError("capacity_blocks is smaller than the blocks present")
     f32 = dict(dtype=torch.float32, device=keys.device)
     st = BlockStats(torch.empty((cap, hkv, d), **f32), torch.empty((cap, hkv), **f32),
                     torch.empty((cap, hkv), **f32))
-    return st.update(keys, 0, nb)
+    return st.update(keys, 0, nb, pages=pages)
 
 
 class CachedDecodeLayer(DecodeLayer):
