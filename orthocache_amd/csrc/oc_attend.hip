@@ -74,24 +74,35 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* s_wave, int& tot
   return before + incl - v;
 }
 
-// s_off[list] = first item of the list, s_off[nlists] = total items.
+// Work-item offsets of the enumeration units: with unified lists (one list
+// per segment, shared by its kv heads) a unit is a segment and its items run
+// head-fastest; with per-head lists a unit is one (segment, head) list.
+// s_off[u] = first item of unit u, s_off[units] = total items.
+__device__ __forceinline__ int num_units(const AttendParams& p) {
+  return p.per_head ? p.num_segments * p.num_kv_heads : p.num_segments;
+}
+
+__device__ __forceinline__ int unit_items(const AttendParams& p, int u, int nqg) {
+  if (p.per_head) return list_count(p, u) * p.nchunk * nqg;
+  return list_count(p, u * p.num_kv_heads) * p.nchunk * nqg * p.num_kv_heads;
+}
+
 __device__ int build_item_offsets(const AttendParams& p, int* s_off, int nqg) {
   __shared__ int s_wave[16];
-  const int nlists = p.num_segments * p.num_kv_heads;
+  const int nu = num_units(p);
   const int t = threadIdx.x;
-  const int per = (nlists + blockDim.x - 1) / blockDim.x;
-  const int lo = min(t * per, nlists);
-  const int hi = min(lo + per, nlists);
-  const int mult = p.nchunk * nqg;
+  const int per = (nu + blockDim.x - 1) / blockDim.x;
+  const int lo = min(t * per, nu);
+  const int hi = min(lo + per, nu);
   int sum = 0;
-  for (int i = lo; i < hi; ++i) sum += list_count(p, i) * mult;
+  for (int i = lo; i < hi; ++i) sum += unit_items(p, i, nqg);
   int total;
   int run = block_exclusive_scan(sum, s_wave, total);
   for (int i = lo; i < hi; ++i) {
     s_off[i] = run;
-    run += list_count(p, i) * mult;
+    run += unit_items(p, i, nqg);
   }
-  if (t == 0) s_off[nlists] = total;
+  if (t == 0) s_off[nu] = total;
   __syncthreads();
   return total;
 }
@@ -162,12 +173,11 @@ __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendPar
 
   const int nq_total = p.sq * p.group;
   const int nqg = (nq_total + kQG - 1) / kQG;
-  const int nlists = p.num_segments * p.num_kv_heads;
-  // One segment with one list shared by the heads: every list has the same
-  // length, so no prefix is needed.
-  const bool uniform_lists = !p.per_head && p.num_segments == 1;
-  const int ipl = uniform_lists ? min(max(p.counts[0], 0), p.total_blocks) * p.nchunk * nqg : 0;
-  const int total_items = uniform_lists ? ipl * nlists : build_item_offsets(p, s_off, nqg);
+  const int H = p.num_kv_heads;
+  // One segment with one list shared by the heads: no prefix is needed.
+  const bool one_unit = !p.per_head && p.num_segments == 1;
+  const int total_items = one_unit ? min(max(p.counts[0], 0), p.total_blocks) * p.nchunk * nqg * H
+                                   : build_item_offsets(p, s_off, nqg);
 
   const int t = threadIdx.x;
   const int cc = t % LPR;
@@ -175,15 +185,21 @@ __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendPar
   const int wave = t / kWave;
 
   for (int item = blockIdx.x; item < total_items; item += gridDim.x) {
-    // Uniform lists are enumerated head-fastest, so concurrently running
-    // workgroups read the other heads' pieces of the same token rows (whole
-    // rows of the (seq, heads, dim) layout, as the scoring kernel does).
+    // Unified lists are enumerated head-fastest within their segment, so
+    // concurrently running workgroups read the other heads' pieces of the
+    // same token rows (whole rows of the (seq, heads, dim) layout, as the
+    // scoring kernel does).  Per-head lists go list by list.
     int list, r0;
-    if (uniform_lists) {
-      list = item % nlists;
-      r0 = item / nlists;
+    if (!p.per_head) {
+      int seg0 = 0, r = item;
+      if (!one_unit) {
+        seg0 = find_list(s_off, p.num_segments, item);
+        r = item - s_off[seg0];
+      }
+      list = seg0 * H + r % H;
+      r0 = r / H;
     } else {
-      list = find_list(s_off, nlists, item);
+      list = find_list(s_off, p.num_segments * H, item);
       r0 = item - s_off[list];
     }
     const int qg = r0 % nqg; r0 /= nqg;
@@ -385,14 +401,14 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
   const int qg = qi / kQG, ql = qi - qg * kQG;
   const int list = seg * p.num_kv_heads + h;
   const int n = list_count(p, list) * p.nchunk;
-  const bool uniform_lists = !p.per_head && p.num_segments == 1;
-  const int base = uniform_lists ? 0 : s_off[list];
-  // Item of the list's j-th (slot, chunk) for query group qg: list-major
-  // offsets in general, head-fastest for uniform lists (as the attention
-  // kernel enumerates them).
+  // Item of the list's j-th (slot, chunk) for query group qg, as the
+  // attention kernel enumerates them: head-fastest within the segment for
+  // unified lists, list by list for per-head lists.
+  const int H = p.num_kv_heads;
+  const bool one_unit = !p.per_head && p.num_segments == 1;
+  const int base = one_unit ? 0 : s_off[p.per_head ? list : seg];
   auto item_of = [&](int j) -> int64_t {
-    return uniform_lists ? ((int64_t)(j * nqg + qg) * (p.num_segments * p.num_kv_heads) + list)
-                         : (int64_t)(base + j * nqg + qg);
+    return p.per_head ? (int64_t)(base + j * nqg + qg) : (int64_t)base + (int64_t)(j * nqg + qg) * H + h;
   };
   const int t = threadIdx.x;
   const int lane = t & (kWave - 1);
