@@ -254,21 +254,24 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
 // score_kernel.  Writes the full bound tensor (Sq*G, nb, Hkv) and/or the
 // per-query-tile NaN-propagating max (ntiles, nb, Hkv), ntiles = ceil(Sq*G/64).
 //
-// q and kbar are staged in LDS transposed ([d][query], [d][block], fp32) in
-// chunks of 64 dims; each thread holds a 4 x 4 (query x block) tile of dot
-// products plus its 4 queries' squared norms, so one pair of 16-byte LDS reads
-// feeds 20 FMAs.  Every dot product accumulates over d in order, as a plain
-// loop would.
+// The q.kbar products are a small GEMM per kv head, done on the fp32 matrix
+// cores (v_mfma_f32_32x32x2_f32, fp32 inputs and accumulation): each wave
+// computes a 32 x 32 (query x block) tile.  Lane l supplies query row l % 32
+// and block row l % 32; its k index runs over its own half of head_dim (the
+// contraction order is free as long as A and B agree), so each lane reads two
+// contiguous half-rows.  The lane's squared query norm comes from the same
+// values.  Output lane l, i: query 8(i/4) + 4(l/32) + i%4, block l % 32.
 constexpr int kBoundQT = 64;
 constexpr int kBoundBT = 64;
-constexpr int kBoundDC = 64;
-constexpr int kBoundPad = 4;
+constexpr int kBoundKC = 32;  // head_dim elements per lane per chunk
 
-template <int QDT>
+// VECLD: q and dc rows are 16-byte aligned and each half-row is a whole number
+// of 16-byte chunks (checked on the host), so a chunk takes 16-byte loads.
+template <int QDT, bool VECLD>
 __global__ __launch_bounds__(256) void bound_kernel(BoundParams p) {
   using EQ = Elt<QDT>;
-  __shared__ __align__(16) float s_q[kBoundDC][kBoundQT + kBoundPad];
-  __shared__ __align__(16) float s_k[kBoundDC][kBoundBT + kBoundPad];
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  __shared__ float s_m[2][2][32];
   const int D = p.head_dim;
   const int H = p.num_kv_heads;
   const int nb = p.num_blocks;
@@ -279,87 +282,100 @@ __global__ __launch_bounds__(256) void bound_kernel(BoundParams p) {
   const int bt = id % nbt;
   const int qt = id / nbt;
   const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int wave = t / kWave;
+  const int wq = wave & 1, wb = wave >> 1;
+  const int r = lane & 31, hf = lane >> 5;
 
-  // Staging role: query / block row r of the tile, dims e0 + 4 j of a chunk.
-  const int r = t & 63, e0 = t >> 6;
-  const int qs = qt * kBoundQT + r;
-  const bool q_ok = qs < nq;
-  const int qc = min(qs, nq - 1);
+  const int qrow = qt * kBoundQT + wq * 32 + r;
+  const int qc = min(qrow, nq - 1);
   const int st = qc / p.group, gq = qc - st * p.group;
   const int64_t qoff = (int64_t)st * p.q_tok_stride + (int64_t)(h * p.group + gq) * p.q_head_stride;
-  const int bs = bt * kBoundBT + r;
-  const bool b_ok = bs < nb;
-  const float* dcrow = p.dc + ((int64_t)min(bs, nb - 1) * H + h) * D;
+  const int brow = bt * kBoundBT + wb * 32 + r;
+  const float* dcrow = p.dc + ((int64_t)min(brow, nb - 1) * H + h) * D;
+  const float eac = p.e_ac[(int64_t)min(brow, nb - 1) * H + h];
 
-  // Compute role: queries 4 tq .. +3, blocks 4 tb .. +3 of the tile.
-  const int tq = t & 15, tb = t >> 4;
-  float eac[4];
+  const int half = (D + 1) / 2;
+  const int d0 = hf * half;
+  const int d1 = min(d0 + half, D);
+  f32x16 acc, acc2;  // two interleaved chains (even / odd k), summed at the end
 #pragma unroll
-  for (int j = 0; j < 4; ++j) eac[j] = p.e_ac[(int64_t)min(bt * kBoundBT + 4 * tb + j, nb - 1) * H + h];
-  float acc[4][4], qq[4];
+  for (int i = 0; i < 16; ++i) { acc[i] = 0.f; acc2[i] = 0.f; }
+  float qq = 0.f;
+  for (int c0 = 0; c0 < half; c0 += kBoundKC) {
+    float qa[kBoundKC], kb[kBoundKC];
+    if constexpr (VECLD) {
+      // Chunks of 16 bytes; the last chunk of a half-row may run past it
+      // (clamped to the row's last chunk and zeroed).
+      constexpr int QV = EQ::VEC;  // q elements per 16-byte load
+      constexpr int QSZ = (QDT == kF32) ? 4 : 2;
+      const char* qb = reinterpret_cast<const char*>(p.q) + qoff * QSZ;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    qq[i] = 0.f;
+      for (int j = 0; j < kBoundKC; j += QV) {
+        const int d = d0 + c0 + j;
+        const int dd = d < d1 ? d : d1 - QV;
+        float tmp[QV];
+        EQ::unpack(ld16(qb + (int64_t)dd * QSZ), tmp);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
-  }
-
-  for (int d0 = 0; d0 < D; d0 += kBoundDC) {
-    float qv[16], kv[16];
+        for (int e = 0; e < QV; ++e) qa[j + e] = d < d1 ? tmp[e] : 0.f;
+      }
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int d = min(d0 + e0 + 4 * j, D - 1);
-      qv[j] = EQ::load1(p.q, qoff + d);
-      kv[j] = dcrow[d];
-    }
-    __syncthreads();  // the previous chunk has been consumed
+      for (int j = 0; j < kBoundKC; j += 4) {
+        const int d = d0 + c0 + j;
+        const int dd = d < d1 ? d : d1 - 4;
+        const float4 kv = *reinterpret_cast<const float4*>(dcrow + dd);
+        const float kvv[4] = {kv.x, kv.y, kv.z, kv.w};
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const bool ok = d0 + e0 + 4 * j < D;
-      s_q[e0 + 4 * j][r] = (ok && q_ok) ? qv[j] : 0.f;
-      s_k[e0 + 4 * j][r] = (ok && b_ok) ? kv[j] / kSqrt512 : 0.f;  // kbar, spectral_energy.py:166
-    }
-    __syncthreads();
-#pragma unroll 8
-    for (int dd = 0; dd < kBoundDC; ++dd) {
-      const float4 a = *reinterpret_cast<const float4*>(&s_q[dd][4 * tq]);
-      const float4 b = *reinterpret_cast<const float4*>(&s_k[dd][4 * tb]);
-      const float av[4] = {a.x, a.y, a.z, a.w};
-      const float bv[4] = {b.x, b.y, b.z, b.w};
+        for (int e = 0; e < 4; ++e) kb[j + e] = d < d1 ? kvv[e] / kSqrt512 : 0.f;  // kbar, spectral_energy.py:166
+      }
+    } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        qq[i] = fmaf(av[i], av[i], qq[i]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+      for (int j = 0; j < kBoundKC; ++j) {
+        const int d = d0 + c0 + j;
+        const bool ok = d < d1;
+        const int dd = ok ? d : D - 1;
+        const float qv = EQ::load1(p.q, qoff + dd);
+        const float kv = dcrow[dd];
+        qa[j] = ok ? qv : 0.f;
+        kb[j] = ok ? kv / kSqrt512 : 0.f;  // kbar, spectral_energy.py:166
       }
     }
+#pragma unroll
+    for (int j = 0; j < kBoundKC; j += 2) {
+      qq = fmaf(qa[j], qa[j], qq);
+      qq = fmaf(qa[j + 1], qa[j + 1], qq);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[j], kb[j], acc, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[j + 1], kb[j + 1], acc2, 0, 0, 0);
+    }
   }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] += acc2[i];
+  qq += __shfl_xor(qq, 32, kWave);  // full squared norm of query row r
 
-  // tau_j(q) = q.kbar/sqrt(d) + ||q|| sqrt(E_AC)/sqrt(d) (spectral_energy.py:170-176);
-  // NaN-propagating max over the tile's queries.
+  // tau_j(q) = q.kbar/sqrt(d) + ||q|| sqrt(E_AC)/sqrt(d) (spectral_energy.py:170-176).
   const float sqrt_d = sqrtf((float)D);
-  float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  const float sqrt_eac = sqrtf(eac);
+  const int b = bt * kBoundBT + wb * 32 + r;
+  float m = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int qi = qt * kBoundQT + 4 * tq + i;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int b = bt * kBoundBT + 4 * tb + j;
-      if (qi < nq && b < nb) {
-        const float bound = acc[i][j] / sqrt_d + (sqrtf(qq[i]) * sqrtf(eac[j])) / sqrt_d;
-        if (p.bounds) p.bounds[((int64_t)qi * nb + b) * H + h] = bound;
-        m[j] = nanmax(m[j], bound);
-      }
+  for (int i = 0; i < 16; ++i) {
+    const int rr = 8 * (i >> 2) + 4 * hf + (i & 3);
+    const float qn = __shfl(qq, rr, kWave);
+    const int qi = qt * kBoundQT + wq * 32 + rr;
+    if (qi < nq && b < nb) {
+      const float bound = acc[i] / sqrt_d + (sqrtf(qn) * sqrt_eac) / sqrt_d;
+      if (p.bounds) p.bounds[((int64_t)qi * nb + b) * H + h] = bound;
+      m = nanmax(m, bound);
     }
   }
   if (p.tau_part) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) m[j] = nanmax(m[j], __shfl_xor(m[j], o, 16));
-      const int b = bt * kBoundBT + 4 * tb + j;
-      if (tq == 0 && b < nb) p.tau_part[((int64_t)qt * nb + b) * H + h] = m[j];
-    }
+    // NaN-propagating max over the tile's 64 queries: the two lane halves,
+    // then the two query-half waves through LDS.
+    m = nanmax(m, __shfl_xor(m, 32, kWave));
+    if (hf == 0) s_m[wb][wq][r] = m;
+    __syncthreads();
+    if (wq == 0 && hf == 0 && b < nb)
+      p.tau_part[((int64_t)qt * nb + b) * H + h] = nanmax(s_m[wb][0][r], s_m[wb][1][r]);
   }
 }
 
@@ -511,16 +527,30 @@ hipError_t launch_score(const ScoreParams& p, hipStream_t s) {
   }
 }
 
+template <int QDT>
+static void launch_bound_q(const BoundParams& p, dim3 grid, bool vec, hipStream_t s) {
+  if (vec) {
+    hipLaunchKernelGGL((bound_kernel<QDT, true>), grid, dim3(256), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((bound_kernel<QDT, false>), grid, dim3(256), 0, s, p);
+  }
+}
+
 hipError_t launch_bound(const BoundParams& p, hipStream_t s) {
   const int nq = p.sq * p.group;
   if (nq == 0 || p.num_blocks == 0) return hipSuccess;
   const int nqt = (nq + kBoundQT - 1) / kBoundQT;
   const int nbt = (p.num_blocks + kBoundBT - 1) / kBoundBT;
   const dim3 grid(nqt * nbt * p.num_kv_heads);
+  const int qsz = p.q_dtype == kF32 ? 4 : 2;
+  const int half = (p.head_dim + 1) / 2;
+  const bool vec = (reinterpret_cast<uintptr_t>(p.q) % 16 == 0) && (reinterpret_cast<uintptr_t>(p.dc) % 16 == 0) &&
+                   (p.q_tok_stride * qsz) % 16 == 0 && (p.q_head_stride * qsz) % 16 == 0 &&
+                   p.head_dim % 2 == 0 && (half * qsz) % 16 == 0 && (half * 4) % 16 == 0;
   switch (p.q_dtype) {
-    case kF32: hipLaunchKernelGGL(bound_kernel<kF32>, grid, dim3(256), 0, s, p); break;
-    case kBF16: hipLaunchKernelGGL(bound_kernel<kBF16>, grid, dim3(256), 0, s, p); break;
-    case kF16: hipLaunchKernelGGL(bound_kernel<kF16>, grid, dim3(256), 0, s, p); break;
+    case kF32: launch_bound_q<kF32>(p, grid, vec, s); break;
+    case kBF16: launch_bound_q<kBF16>(p, grid, vec, s); break;
+    case kF16: launch_bound_q<kF16>(p, grid, vec, s); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
