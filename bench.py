@@ -180,16 +180,36 @@ def main():
     nb = s // 512
     esz = wl.k.element_size()
     q_bytes = wl.q.numel() * wl.q.element_size()
-    score_bytes = s * hkv * d * esz + q_bytes + nb * hkv * 8
+    out_bytes = wl.q.numel() * 2
+    nq = wl.q.shape[-3] * (wl.q.shape[-2] // hkv)
+    # The layer's byte model (the metric's): keys read once by the scoring,
+    # then the retained blocks' keys and values read by the attention.
+    kv_retained = num_active * 512 * hkv * d * esz
     compact_bytes = nb * hkv * 8 + nb * 4 + 4
-    attend_bytes = num_active * 512 * hkv * d * esz * 2 + q_bytes + wl.q.numel() * 2
-    layer_bytes = score_bytes + compact_bytes + attend_bytes
+    layer_bytes = (s * hkv * d * esz + q_bytes + nb * hkv * 8) + compact_bytes + (2 * kv_retained + q_bytes + out_bytes)
+    # What this build's kernels move: with scoring-pass logits the scoring
+    # kernel also writes the fp32 logits of every key row, and the attention
+    # reads the retained values and logits instead of keys and values.
+    logits = _ops.layer_uses_logits(wl.k.dtype, d, nq)
+    nqp = _ops.logits_nq_pad(nq)
+    logit_bytes = nb * hkv * 512 * nqp * 4 if logits else 0
+    score_bytes = s * hkv * d * esz + q_bytes + nb * hkv * 8 + logit_bytes
+    if logits:
+        attend_bytes = kv_retained + num_active * hkv * 512 * nqp * 4 + out_bytes
+    else:
+        attend_bytes = 2 * kv_retained + q_bytes + out_bytes
+    moved_bytes = score_bytes + compact_bytes + attend_bytes
     score_gbs = score_bytes / (score_us * 1e-6) / 1e9
+    # score_kernel<key dtype, lanes per row, query dtype, logit query slots>
+    kernel = f"score_kernel<bf16, 32, bf16, {nqp if logits else 0}>"
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "score_kernel_c2_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("bytes_per_launch")
+            tj = json.load(f)
+        # Counters measured for this very kernel variant only.
+        if tj.get("kernel") == kernel:
+            traffic = tj.get("bytes_per_launch")
 
     result = {
         "metric": METRIC,
@@ -211,10 +231,11 @@ def main():
         "layer_frac_of_peak": round(layer_bytes / (us_per_layer * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
         "layer_event_us": round(layer_event_us, 2),
         "algorithmic_bytes": {"score": score_bytes, "compact": compact_bytes, "attend": attend_bytes,
-                              "layer": layer_bytes},
+                              "layer": moved_bytes, "layer_model": layer_bytes},
+        "scoring_pass_logits": logits,
         "kernels_us": {"score": round(score_us, 2), "mask_compact": round(compact_us, 2),
                        "attend_and_combine": round(attend_us, 2)},
-        "roofline": {"bound": "hbm", "kernel": "score_kernel<bf16, LPR=32>", "achieved": round(score_gbs, 1),
+        "roofline": {"bound": "hbm", "kernel": kernel, "achieved": round(score_gbs, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(score_gbs / PEAK_HBM_GBS, 4),
                      "traffic": traffic},
     }

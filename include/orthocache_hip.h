@@ -29,6 +29,10 @@
  *    pool size in pages; page numbers outside [0, num_pages) are clamped into
  *    it (the kernels never read outside the pool), as are block-list entries
  *    outside their segment.  (ABI version 2 appended these fields.)
+ *  - Scoring-pass logits (ABI version 3 appended `logits` to oc_score_args
+ *    and oc_attend_args): with at most 4 query rows per kv head, the scoring
+ *    pass can also write the attention logits of every key row it streams,
+ *    and the decode attention can read them instead of the keys.
  */
 #ifndef ORTHOCACHE_HIP_H
 #define ORTHOCACHE_HIP_H
@@ -40,7 +44,7 @@
 extern "C" {
 #endif
 
-#define OC_ABI_VERSION 2
+#define OC_ABI_VERSION 3
 
 #define OC_OK 0
 #define OC_ERR_INVALID_ARGUMENT (-1)
@@ -101,7 +105,15 @@ int oc_block_energy(const void* keys, int32_t keys_dtype, int64_t tok_stride, in
  * (src/orthocache/spectral_energy.py:69-196).  Block size is 512.
  * Every output pointer may be NULL.  Requirements: head_dim * esize a multiple
  * of 16 and head_dim / (16 / esize) in {8,16,32,64,128}; 16-byte aligned keys,
- * strides multiples of 16 bytes. */
+ * strides multiples of 16 bytes.
+ * logits (optional, needs q, 1 <= sq*group <= 4, head_dim / (16 / esize) <=
+ * 64, 16-byte aligned q rows): fp32 (total_blocks, Hkv, 512, nq_pad) with
+ * nq_pad = 1, 2 or 4 (sq*group rounded up to a power of two); entry
+ * [j, h, r, i] = q_i . k_{512 j + r, h} * log2(e) / sqrt(head_dim) for query
+ * row i = t*group + g of kv head h (zero for i >= sq*group).  The logits of
+ * softmax(q.k / sqrt(d)) (src/orthocache/adaptive_attention.py:60-61, :103-104) in the
+ * base-2 form, formed while the keys stream so that oc_attend need not read
+ * the keys again.  No counterpart in the reference. */
 typedef struct oc_score_args {
   const void* keys;
   int32_t keys_dtype;
@@ -122,6 +134,7 @@ typedef struct oc_score_args {
   float* e_ac;
   const int32_t* pages; /* (total_blocks) physical page per block, or NULL */
   int32_t num_pages;    /* pages in the key pool (used when pages != NULL) */
+  float* logits;        /* (total_blocks, Hkv, 512, nq_pad), or NULL (ABI 3) */
 } oc_score_args;
 int oc_score_blocks(const oc_score_args* a, void* stream);
 
@@ -202,6 +215,9 @@ int oc_copy_blocks(const void* src, void* dst, const int32_t* indices, const int
  *    head_dim 64 or 128, block_size a multiple of 64 and at least 32 query
  *    rows (sq * group) per kv head; Q K^T and P V on bf16/fp16 MFMA tiles with
  *    fp32 softmax state, P rounded to the input dtype for the P V product.
+ * logits (ABI 3, optional): the oc_score_blocks logits of the same q, keys
+ * and segments; the decode kernel then reads them and the values only (k may
+ * be NULL).  Needs block_size 512 and 1 <= sq*group <= 4.
  * workspace >= oc_attend_workspace_size(...). */
 typedef struct oc_attend_args {
   const void* q;
@@ -224,6 +240,7 @@ typedef struct oc_attend_args {
   int64_t out_seg_stride, out_tok_stride, out_head_stride;
   const int32_t* pages;    /* (total_blocks) physical page per block, or NULL */
   int32_t num_pages;       /* pages in the key/value pools (used when pages != NULL) */
+  const float* logits;     /* scoring-pass logits, or NULL (ABI 3) */
 } oc_attend_args;
 size_t oc_attend_workspace_size(const oc_attend_args* a);
 int oc_attend(const oc_attend_args* a, void* workspace, size_t workspace_bytes, void* stream);
@@ -244,7 +261,10 @@ int oc_attend_plan(const oc_attend_args* a, int32_t* kernel, int32_t* nsplit);
  * per-segment thresholds.  Optional outputs (tau_max, zeta, mask, indices,
  * num_active) may be NULL, in which case the workspace holds them.
  * Launches scoring, mask + compaction, attention and its combine on the
- * stream.  At most 16 queries per kv head (sq * group).
+ * stream.  At most 16 queries per kv head (sq * group).  With at most 4
+ * (and head_dim / (16 / esize) <= 64) the scoring pass also writes the
+ * attention logits into the workspace and the attention reads only the
+ * values of the retained blocks.
  * workspace >= oc_decode_layer_workspace_size(...). */
 typedef struct oc_layer_args {
   const void* q;

@@ -34,6 +34,10 @@ Pinning (what checks each function independently of its own formula):
 * ``attention_*``: float64 closed-form softmax over the retained tokens, and
   the reference's own C++ CPU attention (``notebooks/phase_d_kaggle.py``
   custom call) when ``oracle/_ref`` has been built from the reference.
+* ``block_logits``: a softmax over the retained blocks' logits, times their
+  values, must reproduce ``attention_active_blocks`` (which the reference's
+  C++ attention pins); the logits of a key equal to the query are
+  ||q||^2 / sqrt(d).
 """
 
 from __future__ import annotations
@@ -276,6 +280,22 @@ def attention_active_blocks(q, k, v, active_blocks, block_size=BLOCK, dtype=np.f
         p /= p.sum(axis=1, keepdims=True)
         out[:, h] = p @ vv[:, h // g]
     return out
+
+
+def block_logits(q, keys, block_size=BLOCK, dtype=np.float64):
+    """Attention logits q.k / sqrt(d) of every key row, per block and kv head.
+
+    The logits of ``adaptive_attention.py:60-61`` (one head) and ``:103-104``
+    (all heads) for every token instead of the retained blocks only.
+    q: (Sq, Hq, D) with Hq a multiple of Hkv; keys: (S, Hkv, D).  Returns
+    (nb, Hkv, block_size, Sq*G) with query row i = t*G + g (query head
+    h*G + g of token t), the folded order of ``fold_gqa``.
+    """
+    s, hkv, d = keys.shape
+    nb = s // block_size
+    qf = fold_gqa(q, hkv).astype(dtype)          # (Sq*G, Hkv, D)
+    kb = keys.astype(dtype).reshape(nb, block_size, hkv, d)
+    return np.einsum("brhd,ihd->bhri", kb, qf) / np.sqrt(dtype(d))
 
 
 def attention_per_head_predicated(q, k, v, block_mask, block_size=BLOCK, dtype=np.float64):

@@ -39,7 +39,7 @@ class ScoreArgs(C.Structure):
                 ("q", _vp), ("q_dtype", _i32), ("q_seg_stride", _i64), ("q_tok_stride", _i64),
                 ("q_head_stride", _i64), ("sq", _i32), ("group", _i32),
                 ("tau_max", _vp), ("zeta", _vp), ("dc", _vp), ("e_low", _vp), ("e_mid", _vp),
-                ("e_high", _vp), ("e_ac", _vp), ("pages", _vp), ("num_pages", _i32)]
+                ("e_high", _vp), ("e_ac", _vp), ("pages", _vp), ("num_pages", _i32), ("logits", _vp)]
 
 
 class BoundArgs(C.Structure):
@@ -70,7 +70,8 @@ class AttendArgs(C.Structure):
                 ("cu_blocks", _vp), ("num_segments", _i32),
                 ("indices", _vp), ("counts", _vp), ("per_head", _i32), ("uniform", _vp),
                 ("out", _vp), ("out_dtype", _i32),
-                ("out_seg_stride", _i64), ("out_tok_stride", _i64), ("out_head_stride", _i64), ("pages", _vp), ("num_pages", _i32)]
+                ("out_seg_stride", _i64), ("out_tok_stride", _i64), ("out_head_stride", _i64), ("pages", _vp), ("num_pages", _i32),
+                ("logits", _vp)]
 
 
 class LayerArgs(C.Structure):

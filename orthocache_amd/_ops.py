@@ -90,20 +90,36 @@ class Scores:
     e_high: torch.Tensor | None = None
     e_ac: torch.Tensor | None = None
     bounds: torch.Tensor | None = None  # (Sq*G, nb, Hkv)
+    logits: torch.Tensor | None = None  # (nb, Hkv, 512, nq_pad): q.k * log2(e)/sqrt(d)
 
 
 INLINE_QUERY_LIMIT = 16
+LOGITS_QUERY_LIMIT = 4  # query rows per kv head for scoring-pass logits
+
+
+def logits_nq_pad(nq: int) -> int:
+    """Query slots per key row in the scoring-pass logits (1, 2 or 4)."""
+    return 1 if nq <= 1 else (2 if nq <= 2 else 4)
+
+
+def layer_uses_logits(kv_dtype: torch.dtype, head_dim: int, nq: int) -> bool:
+    """Whether oc_decode_layer forms the logits in its scoring pass (the
+    condition of the library's score_logits_supported): 1..4 query rows per kv
+    head and at most 64 lanes of 16 bytes per key row."""
+    lanes = head_dim * torch.empty((), dtype=kv_dtype).element_size() // 16
+    return 1 <= nq <= LOGITS_QUERY_LIMIT and lanes <= 64
 
 
 def score(keys: torch.Tensor, q: torch.Tensor | None = None, *, want_bands: bool = False,
           want_bounds: bool = False, want_zeta: bool = True, cu_blocks: torch.Tensor | None = None,
-          num_segments: int = 1, pages: torch.Tensor | None = None) -> Scores:
+          num_segments: int = 1, pages: torch.Tensor | None = None, want_logits: bool = False) -> Scores:
     """One pass over the keys: zeta, bands and (with q) the query-aware bound.
 
     keys: (S, Hkv, D), S a multiple of 512.  q: (Sq, Hq, D) for one segment or
     (B, Sq, Hq, D) with cu_blocks for several.  Small query counts get their
     maximum bound inline; large ones (or want_bounds) go through the tiled
-    bound kernel.
+    bound kernel.  want_logits (at most 4 query rows per kv head): also the
+    attention logits of every key row, formed in the same pass.
     """
     require_gpu(keys, q, cu_blocks)
     keys = _kv_view(keys, "keys")
@@ -148,6 +164,10 @@ def score(keys: torch.Tensor, q: torch.Tensor | None = None, *, want_bands: bool
         res.e_high = torch.empty(tiles, **f32)
     if inline:
         res.tau_max = torch.empty((1,) + tiles, **f32)
+    if want_logits:
+        if not (inline and 1 <= nq <= LOGITS_QUERY_LIMIT):
+            raise ValueError(f"logits need 1..{LOGITS_QUERY_LIMIT} query rows per kv head, got {nq}")
+        res.logits = torch.empty((nb, hkv, BLOCK, logits_nq_pad(nq)), **f32)
     a = N.ScoreArgs()
     a.keys = ptr(keys); a.keys_dtype = dtype_code(keys.dtype)
     a.keys_tok_stride = keys.stride(0); a.keys_head_stride = keys.stride(1)
@@ -163,6 +183,7 @@ def score(keys: torch.Tensor, q: torch.Tensor | None = None, *, want_bands: bool
         a.tau_max = ptr(res.tau_max)
     a.zeta = ptr(res.zeta); a.dc = ptr(res.dc); a.e_low = ptr(res.e_low); a.e_mid = ptr(res.e_mid)
     a.e_high = ptr(res.e_high); a.e_ac = ptr(res.e_ac)
+    a.logits = ptr(res.logits)
     check(lib().oc_score_blocks(C.byref(a), stream_ptr(dev)), "oc_score_blocks")
     if q_ok and not inline:
         if cu_blocks is not None:
@@ -288,12 +309,19 @@ def copy_blocks(src: torch.Tensor, dst: torch.Tensor, indices: torch.Tensor, num
 def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, indices: torch.Tensor, counts: torch.Tensor, *,
            block_size: int = BLOCK, per_head: bool = False, uniform: torch.Tensor | None = None,
            out_dtype: torch.dtype | None = None, cu_blocks: torch.Tensor | None = None,
-           num_segments: int = 1, out: torch.Tensor | None = None, pages: torch.Tensor | None = None) -> torch.Tensor:
+           num_segments: int = 1, out: torch.Tensor | None = None, pages: torch.Tensor | None = None,
+           logits: torch.Tensor | None = None) -> torch.Tensor:
     """Attention over the listed blocks.  q: (Sq, Hq, D) (or (B, Sq, Hq, D) with
-    cu_blocks); k, v: (S, Hkv, D).  Returns q-shaped output in out_dtype."""
+    cu_blocks); k, v: (S, Hkv, D).  Returns q-shaped output in out_dtype.
+    logits: the ``score(..., want_logits=True)`` logits of the same q and keys;
+    the keys are then not read."""
     a, out, q = _attend_args(q, k, v, indices, counts, block_size=block_size, per_head=per_head, uniform=uniform,
                              out_dtype=out_dtype, cu_blocks=cu_blocks, num_segments=num_segments, out=out,
                              pages=pages)
+    if logits is not None:
+        if logits.dtype != torch.float32 or not logits.is_contiguous() or logits.shape[:3] != (a.total_blocks, a.num_kv_heads, BLOCK):
+            raise ValueError("logits must be the contiguous fp32 (blocks, kv_heads, 512, nq_pad) output of score()")
+        a.logits = ptr(logits)
     L = lib()
     ws_bytes = int(L.oc_attend_workspace_size(C.byref(a)))
     if ws_bytes == 0 and a.total_blocks > 0:
@@ -459,6 +487,14 @@ class DecodeLayer:
                   "out_seg_stride", "out_tok_stride", "out_head_stride", "pages", "num_pages"):
             setattr(ta, f, getattr(a, f))
         ta.block_size = BLOCK; ta.indices = a.indices; ta.counts = a.num_active
+        # The fused layer forms the attention logits in its scoring pass when
+        # it can; the phases do the same, so each phase times the layer's kernel.
+        self._phase_logits = None
+        if layer_uses_logits(self.k.dtype, a.head_dim, a.sq * a.group):
+            self._phase_logits = torch.empty((a.total_blocks, a.num_kv_heads, BLOCK, logits_nq_pad(a.sq * a.group)),
+                                             dtype=torch.float32, device=self.device)
+            sa.logits = ptr(self._phase_logits)
+            ta.logits = ptr(self._phase_logits)
         ws = int(L.oc_attend_workspace_size(C.byref(ta)))
         self._phase_ws = torch.empty((max(ws, 1),), dtype=torch.uint8, device=self.device)
         self._phase_args = (sa, ca, ta)

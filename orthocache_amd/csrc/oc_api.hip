@@ -41,6 +41,20 @@ int check_kv(const char* name, const void* p, int dt, int64_t tok_stride, int64_
   return OC_OK;
 }
 
+// The scoring kernel addresses a 64-row group of a tile with 32-bit lane
+// offsets: 64 key rows must span less than 2 GiB.
+bool score_rows_fit(int64_t tok_stride, int dt) { return tok_stride >= 0 && tok_stride * esize(dt) * 64 < (1LL << 31); }
+
+float logit_scale_for(int head_dim) { return (float)(1.4426950408889634 / std::sqrt((double)head_dim)); }
+
+// q as the 16-byte row loads of the logits and attention kernels read it.
+int check_q16(const void* q, int dt, int64_t seg_stride, int64_t tok_stride, int64_t head_stride) {
+  const int qs = esize(dt);
+  if (!aligned16(q) || (tok_stride * qs) % 16 || (head_stride * qs) % 16 || (seg_stride * qs) % 16)
+    return fail(OC_ERR_INVALID_ARGUMENT, "q must be 16-byte aligned with 16-byte multiple strides");
+  return OC_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -90,6 +104,9 @@ int oc_score_blocks(const oc_score_args* a, void* stream) {
                 a->head_dim, a->keys_dtype);
   if (a->num_kv_heads <= 0 || a->total_blocks < 0) return fail(OC_ERR_INVALID_ARGUMENT, "bad shape");
   if ((int64_t)a->total_blocks * a->num_kv_heads > 0x7fffffffLL) return fail(OC_ERR_UNSUPPORTED, "too many tiles");
+  if (!score_rows_fit(a->keys_tok_stride, a->keys_dtype))
+    return fail(OC_ERR_UNSUPPORTED, "keys token stride %lld too large (64 rows must span < 2 GiB)",
+                (long long)a->keys_tok_stride);
   if (a->cu_blocks && a->num_segments <= 0) return fail(OC_ERR_INVALID_ARGUMENT, "cu_blocks needs num_segments > 0");
   if (a->q) {
     if (!valid_dtype(a->q_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "q: unknown dtype");
@@ -100,11 +117,20 @@ int oc_score_blocks(const oc_score_args* a, void* stream) {
       return fail(OC_ERR_UNSUPPORTED, "at most 4096 segments per call");
   }
   if (a->pages && a->num_pages <= 0) return fail(OC_ERR_INVALID_ARGUMENT, "pages given with num_pages %d", a->num_pages);
+  if (a->logits) {
+    if (!a->q) return fail(OC_ERR_INVALID_ARGUMENT, "logits need q");
+    if (!oc::score_logits_supported(a->keys_dtype, a->head_dim, a->sq * a->group))
+      return fail(OC_ERR_UNSUPPORTED, "logits: %d query rows per kv head, head_dim %d unsupported (1..%d rows)",
+                  a->sq * a->group, a->head_dim, oc::kLogitsMaxQ);
+    if (!aligned16(a->logits)) return fail(OC_ERR_INVALID_ARGUMENT, "logits must be 16-byte aligned");
+    rc = check_q16(a->q, a->q_dtype, a->cu_blocks ? a->q_seg_stride : 0, a->q_tok_stride, a->q_head_stride);
+    if (rc) return rc;
+  }
   oc::ScoreParams p{a->keys, a->keys_tok_stride, a->keys_head_stride, a->keys_dtype, a->head_dim,
                     a->num_kv_heads, a->total_blocks, a->cu_blocks, a->cu_blocks ? a->num_segments : 1,
                     a->q, a->q_dtype, a->q_seg_stride, a->q_tok_stride, a->q_head_stride, a->sq, a->group,
                     a->tau_max, a->zeta, a->dc, a->e_low, a->e_mid, a->e_high, a->e_ac, a->pages,
-                    a->num_pages};
+                    a->num_pages, a->logits, logit_scale_for(a->head_dim)};
   return hip_check(oc::launch_score(p, (hipStream_t)stream), "oc_score_blocks");
 }
 
@@ -162,7 +188,8 @@ int oc_copy_blocks(const void* src, void* dst, const int32_t* indices, const int
 namespace {
 
 int make_attend_params(const oc_attend_args* a, oc::AttendParams& p) {
-  int rc = check_kv("k", a->k, a->kv_dtype, a->k_tok_stride, a->k_head_stride, a->head_dim);
+  // With scoring-pass logits the keys are not read.
+  int rc = a->logits ? OC_OK : check_kv("k", a->k, a->kv_dtype, a->k_tok_stride, a->k_head_stride, a->head_dim);
   if (rc) return rc;
   rc = check_kv("v", a->v, a->kv_dtype, a->v_tok_stride, a->v_head_stride, a->head_dim);
   if (rc) return rc;
@@ -172,10 +199,14 @@ int make_attend_params(const oc_attend_args* a, oc::AttendParams& p) {
   if (!valid_dtype(a->q_dtype) || !valid_dtype(a->out_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "unknown dtype");
   if (a->q_dtype != a->kv_dtype && a->q_dtype != OC_F32)
     return fail(OC_ERR_UNSUPPORTED, "q dtype must equal the kv dtype or be fp32");
-  {
-    const int qs = esize(a->q_dtype);
-    if (!aligned16(a->q) || (a->q_tok_stride * qs) % 16 || (a->q_head_stride * qs) % 16 || (a->q_seg_stride * qs) % 16)
-      return fail(OC_ERR_INVALID_ARGUMENT, "q must be 16-byte aligned with 16-byte multiple strides");
+  rc = check_q16(a->q, a->q_dtype, a->q_seg_stride, a->q_tok_stride, a->q_head_stride);
+  if (rc) return rc;
+  if (a->logits) {
+    if (a->block_size != OC_BLOCK)
+      return fail(OC_ERR_INVALID_ARGUMENT, "logits: block_size must be %d", OC_BLOCK);
+    if (a->sq * a->group < 1 || a->sq * a->group > oc::kLogitsMaxQ)
+      return fail(OC_ERR_UNSUPPORTED, "logits: %d query rows per kv head (1..%d)", a->sq * a->group, oc::kLogitsMaxQ);
+    if (!aligned16(a->logits)) return fail(OC_ERR_INVALID_ARGUMENT, "logits must be 16-byte aligned");
   }
   if (a->num_kv_heads <= 0 || a->group <= 0 || a->sq < 0 || a->block_size <= 0 || a->total_blocks < 0)
     return fail(OC_ERR_INVALID_ARGUMENT, "bad shape");
@@ -196,15 +227,16 @@ int make_attend_params(const oc_attend_args* a, oc::AttendParams& p) {
   p.block_size = a->block_size; p.total_blocks = a->total_blocks;
   p.cu_blocks = a->cu_blocks; p.num_segments = nseg;
   p.indices = a->indices; p.counts = a->counts; p.per_head = a->per_head; p.uniform = a->uniform;
-  p.logit_scale = (float)(1.4426950408889634 / std::sqrt((double)a->head_dim));
+  p.logit_scale = logit_scale_for(a->head_dim);
   p.chunk = chunk; p.nchunk = (a->block_size + chunk - 1) / chunk;
   p.part_o = nullptr; p.part_ml = nullptr;
   p.out = a->out; p.out_dtype = a->out_dtype;
   p.out_seg_stride = a->out_seg_stride; p.out_tok_stride = a->out_tok_stride; p.out_head_stride = a->out_head_stride;
   p.pages = a->pages; p.num_pages = a->num_pages;
+  p.logits = a->logits;
   p.prefill = oc::prefill_supported(a->kv_dtype, a->q_dtype, a->head_dim, a->sq * a->group, a->block_size) ? 1 : 0;
   // The prefill kernel keeps per-thread offsets inside a 64-token tile in 32 bits.
-  if (a->k_tok_stride >= (1 << 24) || a->v_tok_stride >= (1 << 24)) p.prefill = 0;
+  if (a->k_tok_stride >= (1 << 24) || a->v_tok_stride >= (1 << 24) || a->logits) p.prefill = 0;
   p.nsplit = p.prefill ? oc::prefill_nsplit(p) : 0;
   return OC_OK;
 }
@@ -265,11 +297,17 @@ int oc_attend(const oc_attend_args* a, void* workspace, size_t workspace_bytes, 
 namespace {
 
 struct LayerWs {
-  size_t tau, zeta, idx, cnt, attend, total;
+  size_t tau, zeta, idx, cnt, logits, attend, total;
 };
 
-// Workspace: [tau_max | zeta | indices | num_active | attention partials].
-LayerWs layer_ws_layout(const oc_layer_args* a, size_t attend_bytes) {
+// True when the layer's scoring pass also writes the attention logits (the
+// attention then reads values only).
+bool layer_uses_logits(const oc_layer_args* a) {
+  return oc::score_logits_supported(a->kv_dtype, a->head_dim, a->sq * a->group);
+}
+
+// Workspace: [tau_max | zeta | indices | num_active | logits | attention partials].
+LayerWs layer_ws_layout(const oc_layer_args* a, size_t attend_bytes, bool logits) {
   LayerWs w{};
   const size_t tiles = (size_t)a->total_blocks * a->num_kv_heads;
   const int nseg = a->cu_blocks ? a->num_segments : 1;
@@ -278,6 +316,8 @@ LayerWs layer_ws_layout(const oc_layer_args* a, size_t attend_bytes) {
   w.zeta = off; off += a->zeta ? 0 : align256(tiles * 4);
   w.idx = off; off += a->indices ? 0 : align256((size_t)a->total_blocks * 4);
   w.cnt = off; off += a->num_active ? 0 : align256((size_t)nseg * 4);
+  w.logits = off;
+  off += logits ? align256(tiles * OC_BLOCK * oc::logits_nq_pad(a->sq * a->group) * sizeof(float)) : 0;
   w.attend = off; off += attend_bytes;
   w.total = off;
   return w;
@@ -311,7 +351,7 @@ size_t oc_decode_layer_workspace_size(const oc_layer_args* a) {
   oc_attend_args t = layer_attend_args(a);
   oc::AttendParams p;
   if (make_attend_params(&t, p)) return 0;
-  return layer_ws_layout(a, attend_ws(p)).total;
+  return layer_ws_layout(a, attend_ws(p), layer_uses_logits(a)).total;
 }
 
 }  // extern "C"
@@ -333,6 +373,9 @@ int decode_layer_impl(const oc_layer_args* a, const oc_block_stats* st, void* wo
       return fail(OC_ERR_UNSUPPORTED, "%s: head_dim %d unsupported (64, 128, 256 or 512)", name, a->head_dim);
   } else if (!oc::score_supported(a->kv_dtype, a->head_dim)) {
     return fail(OC_ERR_UNSUPPORTED, "scores: head_dim %d unsupported", a->head_dim);
+  } else if (!score_rows_fit(a->k_tok_stride, a->kv_dtype)) {
+    return fail(OC_ERR_UNSUPPORTED, "keys token stride %lld too large (64 rows must span < 2 GiB)",
+                (long long)a->k_tok_stride);
   }
   if (a->q_dtype != a->kv_dtype && a->q_dtype != OC_F32)
     return fail(OC_ERR_UNSUPPORTED, "q dtype must equal the kv dtype or be fp32");
@@ -340,7 +383,8 @@ int decode_layer_impl(const oc_layer_args* a, const oc_block_stats* st, void* wo
     return fail(OC_ERR_UNSUPPORTED, "decode layer takes at most 16 queries per kv head (sq * group)");
   const int nseg = a->cu_blocks ? a->num_segments : 1;
   if (a->cu_blocks && nseg > 4096) return fail(OC_ERR_UNSUPPORTED, "at most 4096 segments per call");
-  const LayerWs w = layer_ws_layout(a, attend_ws(ap));
+  const bool use_logits = !st && layer_uses_logits(a);
+  const LayerWs w = layer_ws_layout(a, attend_ws(ap), use_logits);
   if (w.total && (!workspace || workspace_bytes < w.total))
     return fail(OC_ERR_WORKSPACE, "workspace %zu bytes < %zu needed", workspace_bytes, w.total);
   char* ws = static_cast<char*>(workspace);
@@ -373,6 +417,11 @@ int decode_layer_impl(const oc_layer_args* a, const oc_block_stats* st, void* wo
     sp.sq = a->sq; sp.group = a->group;
     sp.tau_max = tau_max; sp.zeta = zeta;
     sp.pages = a->pages; sp.num_pages = a->num_pages;
+    if (use_logits) {
+      sp.logits = reinterpret_cast<float*>(ws + w.logits);
+      sp.logit_scale = ap.logit_scale;
+      ap.logits = sp.logits;
+    }
     rc = hip_check(oc::launch_score(sp, s), "oc_decode_layer scores");
     if (rc) return rc;
     zeta_in = zeta;
@@ -405,7 +454,13 @@ int oc_decode_layer(const oc_layer_args* a, void* workspace, size_t workspace_by
   return decode_layer_impl(a, nullptr, workspace, workspace_bytes, stream, "oc_decode_layer");
 }
 
-size_t oc_decode_layer_cached_workspace_size(const oc_layer_args* a) { return oc_decode_layer_workspace_size(a); }
+size_t oc_decode_layer_cached_workspace_size(const oc_layer_args* a) {
+  if (!a) return 0;
+  oc_attend_args t = layer_attend_args(a);
+  oc::AttendParams p;
+  if (make_attend_params(&t, p)) return 0;
+  return layer_ws_layout(a, attend_ws(p), false).total;
+}
 
 int oc_decode_layer_cached(const oc_layer_args* a, const oc_block_stats* stats, void* workspace,
                            size_t workspace_bytes, void* stream) {

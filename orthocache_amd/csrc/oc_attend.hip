@@ -29,6 +29,12 @@
 //
 // Logits are kept in the log2 domain: s2 = q.k * log2(e) / sqrt(d), weights
 // exp2(s2 - m2); identical to the natural-log form in exact arithmetic.
+//
+// Logits variant (LG): inside the fused decode layer the scoring kernel has
+// already formed every key row's logits while streaming the keys
+// (ScoreParams::logits), so an item reads its rows' logits (NQ floats per
+// row) and the value rows only -- half the bytes of K + V -- and skips the
+// dot products, the butterfly and the LDS logit exchange.
 #include "oc_kernels.h"
 
 #ifndef OC_ATTEND_THREADS
@@ -116,31 +122,6 @@ __device__ __forceinline__ int find_list(const int* s_off, int nlists, int item)
   return lo;
 }
 
-// Halving butterfly over LPR lanes.  With V >= LPR, lane l ends with the full
-// sums of value indices [l*V/LPR, (l+1)*V/LPR) in v[0..V/LPR); with V < LPR,
-// v[0] of lane l is the sum of index l / (LPR/V).
-template <int V, int CNT, int B, int LPR>
-struct Butterfly {
-  __device__ __forceinline__ static void run(float (&v)[V], int lane) {
-    if constexpr (B >= 1) {
-      if constexpr (CNT > 1) {
-        constexpr int H = CNT / 2;
-        const bool upper = (lane & B) != 0;
-#pragma unroll
-        for (int i = 0; i < H; ++i) {
-          const float send = upper ? v[i] : v[i + H];
-          const float keep = upper ? v[i + H] : v[i];
-          v[i] = keep + __shfl_xor(send, B, LPR);
-        }
-        Butterfly<V, H, B / 2, LPR>::run(v, lane);
-      } else {
-        v[0] += __shfl_xor(v[0], B, LPR);
-        Butterfly<V, 1, B / 2, LPR>::run(v, lane);
-      }
-    }
-  }
-};
-
 // Threads per attention workgroup: NSLOT = kAttendThreads / LPR token rows
 // are in flight per load instruction, R per slot per item.
 constexpr int kAttendThreads = OC_ATTEND_THREADS;
@@ -151,7 +132,7 @@ __host__ __device__ constexpr int rows_per_slot() {
   return NQ <= 4 ? 8 : 4;
 }
 
-template <int DT, int LPR, int NQ, int QDT>
+template <int DT, int LPR, int NQ, int QDT, bool LG>
 __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendParams p) {
   using E = Elt<DT>;
   using EQ = Elt<QDT>;
@@ -165,8 +146,9 @@ __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendPar
   constexpr int SPW = kWave / LPR;                // slots per wave
   constexpr int NWAVE = kAttendThreads / kWave;
 
+  static_assert(!LG || NQ <= kLogitsMaxQ, "logits carry at most kLogitsMaxQ queries");
   __shared__ int s_off[kMaxLists + 1];
-  __shared__ float s_log[NSLOT * V];
+  __shared__ float s_log[LG ? 1 : NSLOT * V];
   __shared__ float s_o[NWAVE * NQ * D];
   __shared__ float s_m[NWAVE * NQ];
   __shared__ float s_l[NWAVE * NQ];
@@ -214,81 +196,117 @@ __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendPar
     const int64_t tok0 = page * p.block_size + (int64_t)c * p.chunk;
     const int nrows = min(p.chunk, p.block_size - c * p.chunk);
 
-    const char* kb = reinterpret_cast<const char*>(p.k) +
-                     (tok0 * p.k_tok_stride + (int64_t)h * p.k_head_stride + (int64_t)cc * VEC) * ESZ;
     const char* vb = reinterpret_cast<const char*>(p.v) +
                      (tok0 * p.v_tok_stride + (int64_t)h * p.v_head_stride + (int64_t)cc * VEC) * ESZ;
-    const int64_t krow = p.k_tok_stride * ESZ, vrow = p.v_tok_stride * ESZ;
-
-    // Queries (pre-scaled by log2(e)/sqrt(d)); 16-byte loads of the lane's
-    // VEC elements, query index clamped and missing queries zeroed.  They are
-    // requested before K and V: loads retire in order, so the dot products
-    // then wait only for K while V is still arriving.
-    float qv[NQ][VEC];
-#pragma unroll
-    for (int g = 0; g < NQ; ++g) {
-      const int qi = qg * kQG + g;
-      const int qc = min(qi, nq_total - 1);
-      const int st = qc / p.group, gg = qc - st * p.group;
-      constexpr int QSZ = (QDT == kF32) ? 4 : 2;
-      const char* qp = reinterpret_cast<const char*>(p.q) +
-                       ((int64_t)seg * p.q_seg_stride + (int64_t)st * p.q_tok_stride +
-                        (int64_t)(h * p.group + gg) * p.q_head_stride + (int64_t)cc * VEC) * QSZ;
-      const float sc = qi < nq_total ? p.logit_scale : 0.f;
-#pragma unroll
-      for (int e0 = 0; e0 < VEC; e0 += EQ::VEC) {
-        float tmp[EQ::VEC];
-        EQ::unpack(ld16(qp + e0 * QSZ), tmp);
-#pragma unroll
-        for (int e = 0; e < EQ::VEC && e0 + e < VEC; ++e) qv[g][e0 + e] = tmp[e] * sc;
-      }
-    }
-
-    // Every K and V load of the item, before any arithmetic.  Row indices are clamped
-    // into the block (loads stay unconditional, so none waits behind a
-    // branch) and rows past nrows are masked afterwards.
-    uint4 kw[R], vw[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) kw[r] = ld16_nt(kb + min(slot + NSLOT * r, nrows - 1) * krow);
-#pragma unroll
-    for (int r = 0; r < R; ++r) vw[r] = ld16_nt(vb + min(slot + NSLOT * r, nrows - 1) * vrow);
-
-    // Uniform per workgroup: a scalar load, which does not wait on the K/V loads.
+    const int64_t vrow = p.v_tok_stride * ESZ;
+    // Uniform per workgroup: a scalar load, which does not wait on the vector loads.
     const bool uni = (p.uniform != nullptr) && (p.uniform[list] != 0);
 
-    // Partial dot products, value index r*NQ + g.
-    float part[V];
+    // Logits of the lane's R rows (log2 domain): sl[r][g].
+    float sl[R][NQ];
+    uint4 vw[R];
+    if constexpr (LG) {
+      // From the scoring pass: NQ floats per row of the block's 512 x NQ
+      // tile, rows clamped into the chunk (masked below), then the V rows.
+      const float* lb = p.logits + (((int64_t)(off + blk) * p.num_kv_heads + h) * kBlock +
+                                    (int64_t)c * p.chunk) * NQ;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float kx[VEC];
-      E::unpack(kw[r], kx);
-#pragma unroll
-      for (int g = 0; g < NQ; ++g) {
-        float d = 0.f;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) d = fmaf(qv[g][e], kx[e], d);
-        part[r * NQ + g] = d;
+      for (int r = 0; r < R; ++r) {
+        const float* lp = lb + (int64_t)min(slot + NSLOT * r, nrows - 1) * NQ;
+        if constexpr (NQ == 4) {
+          const float4 w = *reinterpret_cast<const float4*>(lp);
+          sl[r][0] = w.x; sl[r][1] = w.y; sl[r][2] = w.z; sl[r][3] = w.w;
+        } else if constexpr (NQ == 2) {
+          const float2 w = *reinterpret_cast<const float2*>(lp);
+          sl[r][0] = w.x; sl[r][1] = w.y;
+        } else {
+          sl[r][0] = lp[0];
+        }
       }
-    }
-    Butterfly<V, V, LPR / 2, LPR>::run(part, cc);
-
-    // Logits to LDS (invalid rows -inf, uniform lists 0).
-    if constexpr (V >= LPR) {
 #pragma unroll
-      for (int u = 0; u < PER_LANE; ++u) {
-        const int idx = cc * PER_LANE + u;
-        const int row = slot + NSLOT * (idx / NQ);
-        s_log[slot * V + idx] = row < nrows ? (uni ? 0.f : part[u]) : -INFINITY;
+      for (int r = 0; r < R; ++r) vw[r] = ld16_nt(vb + min(slot + NSLOT * r, nrows - 1) * vrow);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const bool ok = slot + NSLOT * r < nrows;
+#pragma unroll
+        for (int g = 0; g < NQ; ++g) sl[r][g] = ok ? (uni ? 0.f : sl[r][g]) : -INFINITY;
       }
     } else {
-      constexpr int REP = LPR / V;
-      if (cc % REP == 0) {
-        const int idx = cc / REP;
-        const int row = slot + NSLOT * (idx / NQ);
-        s_log[slot * V + idx] = row < nrows ? (uni ? 0.f : part[0]) : -INFINITY;
+      const char* kb = reinterpret_cast<const char*>(p.k) +
+                       (tok0 * p.k_tok_stride + (int64_t)h * p.k_head_stride + (int64_t)cc * VEC) * ESZ;
+      const int64_t krow = p.k_tok_stride * ESZ;
+
+      // Queries (pre-scaled by log2(e)/sqrt(d)); 16-byte loads of the lane's
+      // VEC elements, query index clamped and missing queries zeroed.  They are
+      // requested before K and V: loads retire in order, so the dot products
+      // then wait only for K while V is still arriving.
+      float qv[NQ][VEC];
+#pragma unroll
+      for (int g = 0; g < NQ; ++g) {
+        const int qi = qg * kQG + g;
+        const int qc = min(qi, nq_total - 1);
+        const int st = qc / p.group, gg = qc - st * p.group;
+        constexpr int QSZ = (QDT == kF32) ? 4 : 2;
+        const char* qp = reinterpret_cast<const char*>(p.q) +
+                         ((int64_t)seg * p.q_seg_stride + (int64_t)st * p.q_tok_stride +
+                          (int64_t)(h * p.group + gg) * p.q_head_stride + (int64_t)cc * VEC) * QSZ;
+        const float sc = qi < nq_total ? p.logit_scale : 0.f;
+#pragma unroll
+        for (int e0 = 0; e0 < VEC; e0 += EQ::VEC) {
+          float tmp[EQ::VEC];
+          EQ::unpack(ld16(qp + e0 * QSZ), tmp);
+#pragma unroll
+          for (int e = 0; e < EQ::VEC && e0 + e < VEC; ++e) qv[g][e0 + e] = tmp[e] * sc;
+        }
       }
+
+      // Every K and V load of the item, before any arithmetic.  Row indices are clamped
+      // into the block (loads stay unconditional, so none waits behind a
+      // branch) and rows past nrows are masked afterwards.
+      uint4 kw[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) kw[r] = ld16_nt(kb + min(slot + NSLOT * r, nrows - 1) * krow);
+#pragma unroll
+      for (int r = 0; r < R; ++r) vw[r] = ld16_nt(vb + min(slot + NSLOT * r, nrows - 1) * vrow);
+
+      // Partial dot products, value index r*NQ + g.
+      float part[V];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float kx[VEC];
+        E::unpack(kw[r], kx);
+#pragma unroll
+        for (int g = 0; g < NQ; ++g) {
+          float d = 0.f;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) d = fmaf(qv[g][e], kx[e], d);
+          part[r * NQ + g] = d;
+        }
+      }
+      Butterfly<V, V, LPR / 2, LPR>::run(part, cc);
+
+      // Logits to LDS (invalid rows -inf, uniform lists 0).
+      if constexpr (V >= LPR) {
+#pragma unroll
+        for (int u = 0; u < PER_LANE; ++u) {
+          const int idx = cc * PER_LANE + u;
+          const int row = slot + NSLOT * (idx / NQ);
+          s_log[slot * V + idx] = row < nrows ? (uni ? 0.f : part[u]) : -INFINITY;
+        }
+      } else {
+        constexpr int REP = LPR / V;
+        if (cc % REP == 0) {
+          const int idx = cc / REP;
+          const int row = slot + NSLOT * (idx / NQ);
+          s_log[slot * V + idx] = row < nrows ? (uni ? 0.f : part[0]) : -INFINITY;
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int g = 0; g < NQ; ++g) sl[r][g] = s_log[slot * V + r * NQ + g];
     }
-    __syncthreads();
 
     // Per-slot softmax state and P.V.
     float m[NQ], l[NQ], o[NQ][VEC];
@@ -296,7 +314,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendPar
     for (int g = 0; g < NQ; ++g) {
       float mx = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < R; ++r) mx = fmaxf(mx, s_log[slot * V + r * NQ + g]);
+      for (int r = 0; r < R; ++r) mx = fmaxf(mx, sl[r][g]);
       m[g] = mx;
       l[g] = 0.f;
 #pragma unroll
@@ -310,7 +328,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendPar
         E::unpack(vw[r], vx);
 #pragma unroll
         for (int g = 0; g < NQ; ++g) {
-          const float pw = exp2f(s_log[slot * V + r * NQ + g] - m[g]);
+          const float pw = exp2f(sl[r][g] - m[g]);
           l[g] += pw;
 #pragma unroll
           for (int e = 0; e < VEC; ++e) o[g][e] = fmaf(pw, vx[e], o[g][e]);
@@ -465,10 +483,18 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
 
 template <int DT, int LPR, int NQ>
 static hipError_t launch_attend_t(const AttendParams& p, int grid, hipStream_t s) {
+  if (p.logits) {
+    // The queries are already folded into the logits.
+    if constexpr (NQ <= kLogitsMaxQ) {
+      hipLaunchKernelGGL((attend_decode_kernel<DT, LPR, NQ, DT, true>), dim3(grid), dim3(kAttendThreads), 0, s, p);
+      return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
+  }
   if (p.q_dtype == DT) {
-    hipLaunchKernelGGL((attend_decode_kernel<DT, LPR, NQ, DT>), dim3(grid), dim3(kAttendThreads), 0, s, p);
+    hipLaunchKernelGGL((attend_decode_kernel<DT, LPR, NQ, DT, false>), dim3(grid), dim3(kAttendThreads), 0, s, p);
   } else if (p.q_dtype == kF32) {
-    hipLaunchKernelGGL((attend_decode_kernel<DT, LPR, NQ, kF32>), dim3(grid), dim3(kAttendThreads), 0, s, p);
+    hipLaunchKernelGGL((attend_decode_kernel<DT, LPR, NQ, kF32, false>), dim3(grid), dim3(kAttendThreads), 0, s, p);
   } else {
     return hipErrorInvalidValue;
   }

@@ -40,8 +40,14 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
 
 // Element type traits: VEC elements per 16-byte lane load.
 template <int DT> struct Elt;
+// get(w, c): element c of a 16-byte word, widened to fp32 (c is a
+// compile-time constant after unrolling).
+__device__ __forceinline__ uint32_t word_of(const uint4& w, int i) {
+  return i == 0 ? w.x : i == 1 ? w.y : i == 2 ? w.z : w.w;
+}
 template <> struct Elt<kF32> {
   static constexpr int VEC = 4;
+  __device__ __forceinline__ static float get(const uint4& w, int c) { return __uint_as_float(word_of(w, c)); }
   __device__ __forceinline__ static void unpack(const uint4& w, float* o) {
     o[0] = __uint_as_float(w.x); o[1] = __uint_as_float(w.y);
     o[2] = __uint_as_float(w.z); o[3] = __uint_as_float(w.w);
@@ -55,6 +61,9 @@ template <> struct Elt<kF32> {
 };
 template <> struct Elt<kBF16> {
   static constexpr int VEC = 8;
+  __device__ __forceinline__ static float get(const uint4& w, int c) {
+    return (c & 1) ? bf16_hi(word_of(w, c / 2)) : bf16_lo(word_of(w, c / 2));
+  }
   __device__ __forceinline__ static void unpack(const uint4& w, float* o) {
     o[0] = bf16_lo(w.x); o[1] = bf16_hi(w.x); o[2] = bf16_lo(w.y); o[3] = bf16_hi(w.y);
     o[4] = bf16_lo(w.z); o[5] = bf16_hi(w.z); o[6] = bf16_lo(w.w); o[7] = bf16_hi(w.w);
@@ -68,6 +77,9 @@ template <> struct Elt<kBF16> {
 };
 template <> struct Elt<kF16> {
   static constexpr int VEC = 8;
+  __device__ __forceinline__ static float get(const uint4& w, int c) {
+    return f16_bits_to_f32(word_of(w, c / 2) >> (16 * (c & 1)));
+  }
   __device__ __forceinline__ static void unpack(const uint4& w, float* o) {
     o[0] = f16_bits_to_f32(w.x); o[1] = f16_bits_to_f32(w.x >> 16);
     o[2] = f16_bits_to_f32(w.y); o[3] = f16_bits_to_f32(w.y >> 16);
@@ -90,6 +102,21 @@ __device__ __forceinline__ void store_elt(int dt, void* p, int64_t i, float v) {
   if (dt == kF32) Elt<kF32>::store1(p, i, v);
   else if (dt == kBF16) Elt<kBF16>::store1(p, i, v);
   else Elt<kF16>::store1(p, i, v);
+}
+
+// acc + a.lo * b.lo + a.hi * b.hi for two packed 16-bit floats per operand
+// (v_dot2c_f32_bf16 / v_dot2c_f32_f16): the products are exact in fp32 and
+// accumulate in fp32.
+template <int DT>
+__device__ __forceinline__ float dot2_acc(uint32_t a, uint32_t b, float acc) {
+  static_assert(DT == kBF16 || DT == kF16, "16-bit types only");
+  if constexpr (DT == kBF16) {
+    typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, a), __builtin_bit_cast(v2bf, b), acc, false);
+  } else {
+    typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h, a), __builtin_bit_cast(v2h, b), acc, false);
+  }
 }
 
 // 16-byte global load (the caller guarantees 16-byte alignment).
@@ -118,6 +145,33 @@ __device__ __forceinline__ float group_sum(float v) {
 }
 
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<kWave>(v); }
+
+// Halving butterfly: sums V per-lane values over groups of LPR lanes.  With
+// V >= LPR, lane l ends with the full sums of value indices
+// [l*V/LPR, (l+1)*V/LPR) in v[0..V/LPR); with V < LPR, v[0] of lane l is the
+// sum of index l / (LPR/V).  V - 1 shuffles for V values instead of
+// V log2(LPR).  Instantiate as Butterfly<V, V, LPR / 2, LPR>.
+template <int V, int CNT, int B, int LPR>
+struct Butterfly {
+  __device__ __forceinline__ static void run(float (&v)[V], int lane) {
+    if constexpr (B >= 1) {
+      if constexpr (CNT > 1) {
+        constexpr int H = CNT / 2;
+        const bool upper = (lane & B) != 0;
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+          const float send = upper ? v[i] : v[i + H];
+          const float keep = upper ? v[i + H] : v[i];
+          v[i] = keep + __shfl_xor(send, B, LPR);
+        }
+        Butterfly<V, H, B / 2, LPR>::run(v, lane);
+      } else {
+        v[0] += __shfl_xor(v[0], B, LPR);
+        Butterfly<V, 1, B / 2, LPR>::run(v, lane);
+      }
+    }
+  }
+};
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

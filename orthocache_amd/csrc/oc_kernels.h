@@ -135,9 +135,19 @@ struct ScoreParams {
   float* e_ac;
   const int* pages;  // (total_blocks) physical 512-token page of each block, or null (pages = blocks)
   int num_pages;     // pool size in pages (page numbers are clamped into it)
+  // Attention logits of the segment's queries, written while the keys stream
+  // (or null): logits[((gb * Hkv + h) * 512 + row) * nq_pad + i] =
+  // q_i . k_row * logit_scale for query row i < sq*group of kv head h
+  // (0 for i >= sq*group); nq_pad = logits_nq_pad(sq * group) <= kLogitsMaxQ.
+  float* logits;
+  float logit_scale;  // log2(e) / sqrt(head_dim)
 };
 
+constexpr int kLogitsMaxQ = 4;  // query rows per kv head with scoring-pass logits
+__host__ __device__ inline int logits_nq_pad(int nq) { return nq <= 1 ? 1 : (nq <= 2 ? 2 : 4); }
+
 bool score_supported(int dt, int head_dim);
+bool score_logits_supported(int dt, int head_dim, int nq);
 hipError_t launch_score(const ScoreParams& p, hipStream_t s);
 hipError_t launch_copy_blocks(const CopyParams& p, hipStream_t s);
 
@@ -180,6 +190,10 @@ struct AttendParams {
   int64_t out_seg_stride, out_tok_stride, out_head_stride;
   const int* pages;  // (total_blocks) physical page of each block (block_size tokens), or null
   int num_pages;     // pool size in pages (page numbers are clamped into it)
+  // Logits from the scoring pass (ScoreParams::logits layout) or null.  When
+  // set, the decode kernel reads them instead of the keys (block_size 512,
+  // sq*group <= kLogitsMaxQ); k is not read.
+  const float* logits;
 };
 
 bool attend_supported(int dt, int head_dim);

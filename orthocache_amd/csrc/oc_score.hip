@@ -25,20 +25,51 @@
 // Lanes are laid out LPR per token row (16-byte loads along D, coalesced);
 // NSLOT = 256/LPR row slots each walk 64/NSLOT values of l, loading the eight
 // rows 64k + l together.
+//
+// Optionally (NQL > 0, decode with at most 4 query rows per kv head) the same
+// pass also forms the attention logits q.k of every key row it streams: the
+// lane's VEC-element partial dot products of its eight rows are summed over
+// the row's LPR lanes with a halving butterfly, staged in LDS and written as
+// one contiguous 512 x NQL fp32 tile.  The attention then reads only the
+// values of the retained blocks, not their keys a second time.
 #include "oc_kernels.h"
 
 namespace oc {
 
-template <int DT, int LPR>
-__device__ __forceinline__ void load_rows(const char* base, int64_t row_bytes, int l, uint4 (&r)[8]) {
+// Rows 64k + l (k = 0..7) of the tile: a wave-uniform base (tile start plus
+// 64k rows, scalar registers) and the lane's 32-bit offset l * row_bytes +
+// column bytes, so each load takes one address VGPR (global_load saddr form).
+// The host guarantees 64 * row_bytes < 2^31.
+__device__ __forceinline__ void load_rows(const char* tbase, int64_t stride64, uint32_t loff, uint4 (&r)[8]) {
 #pragma unroll
-  for (int k = 0; k < 8; ++k) r[k] = ld16_nt(base + (int64_t)(64 * k + l) * row_bytes);
+  for (int k = 0; k < 8; ++k) r[k] = ld16_nt(tbase + k * stride64 + loff);
 }
 
 constexpr int kMaxSegLds = 4096;  // segments whose offsets are staged in LDS
 
-template <int DT, int LPR, int QDT>
-__global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
+// Segment holding flattened block gb (binary search over cu staged in LDS).
+__device__ __forceinline__ int find_segment(const int* s_cu, int num_segments, int gb) {
+  int lo = 0, hi = num_segments - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_cu[mid] <= gb) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Occupancy target of the logits variants whose registers fit three
+// workgroups per CU without spilling (168 VGPRs): packed dot products
+// (16-bit keys and queries), 32 lanes per row, two query rows.  Measured on
+// the C2 shape (bf16, head_dim 256): 90 us at three workgroups per CU
+// against 97 us at two.
+template <int DT, int LPR, int QDT, int NQL>
+constexpr int score_min_waves() {
+  return (DT != kF32 && QDT == DT && NQL == 2 && LPR == 32) ? 3 : 1;
+}
+
+template <int DT, int LPR, int QDT, int NQL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(score_min_waves<DT, LPR, QDT, NQL>())))
+void score_kernel(ScoreParams p) {
   using E = Elt<DT>;
   using EQ = Elt<QDT>;
   constexpr int VEC = E::VEC;
@@ -47,12 +78,14 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
   constexpr int NLO = 64 / NSLOT;
   static_assert(NLO >= 2 && (NLO % 2) == 0, "unsupported lane layout");
   constexpr int ESZ = (DT == kF32) ? 4 : 2;
+  constexpr int QSZ = (QDT == kF32) ? 4 : 2;
 
   constexpr int NI = (D + 255) / 256;  // head_dim columns per thread in the epilogue
   __shared__ float s_mean[NSLOT * D];
   __shared__ float s_m2[NSLOT * D];
   __shared__ float s_red[64];
   __shared__ int s_cu[kMaxSegLds + 1];
+  __shared__ __attribute__((aligned(16))) float s_lg[NQL > 0 ? kBlock * NQL : 4];
 
   const int tile = blockIdx.x;
   const int H = p.num_kv_heads;
@@ -63,11 +96,13 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
   const int slot = t / LPR;
 
   const int64_t row_bytes = p.k_tok_stride * ESZ;
+  const int64_t stride64 = 64 * row_bytes;
   // Paged caches: the block's keys live in physical page pages[gb].
   const int64_t page = page_of(p.pages, p.num_pages, gb);
-  const char* base = reinterpret_cast<const char*>(p.k) +
-                     (page * kBlock * p.k_tok_stride + (int64_t)h * p.k_head_stride +
-                      (int64_t)cc * VEC) * ESZ;
+  const char* tbase = reinterpret_cast<const char*>(p.k) +
+                      (page * kBlock * p.k_tok_stride + (int64_t)h * p.k_head_stride) * ESZ;
+  // Lane offset of row l within the 64-row group: l * row_bytes + column bytes.
+  auto lane_off = [&](int l) -> uint32_t { return (uint32_t)(l * (uint32_t)row_bytes) + (uint32_t)(cc * VEC * ESZ); };
 
   // Query-aware bound inputs, requested before the key stream so their
   // latency overlaps it: the segment table (ragged batches) goes to LDS, the
@@ -75,7 +110,7 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
   // (one segment; a ragged batch needs the segment id first).
   const bool want_bound = p.q != nullptr && p.tau_max != nullptr;
   const int nq = p.sq * p.group;
-  const bool need_seg = p.cu_blocks != nullptr && want_bound;
+  const bool need_seg = p.cu_blocks != nullptr && (want_bound || NQL > 0);
   if (need_seg) {
     for (int i = t; i <= p.num_segments; i += 256) s_cu[i] = p.cu_blocks[i];
   }
@@ -96,42 +131,144 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
 #pragma unroll
   for (int c = 0; c < VEC; ++c) { acc_hi[c] = 0.f; acc_mid[c] = 0.f; acc_mid2[c] = 0.f; ssum[c] = 0.f; ssq[c] = 0.f; piv[c] = 0.f; }
 
-  auto consume = [&](const uint4 (&r)[8], bool first) {
-    float x[8][VEC];
+  // Logit queries: this lane's VEC columns of each of the kv head's query
+  // rows (rows past nq are zero).  With 16-bit keys and queries of the same
+  // type they stay packed (DOT2: packed dot products on the raw key words,
+  // scaled by log2(e)/sqrt(d) after the lane reduction); otherwise they are
+  // widened and pre-scaled.
+  constexpr bool DOT2 = NQL > 0 && DT != kF32 && QDT == DT;
+  float lq[NQL > 0 && !DOT2 ? NQL : 1][VEC];
+  uint32_t lqw[DOT2 ? NQL : 1][VEC / 2];
+
+  // Band statistics of column c from its values in the eight rows 64k + l.
+  auto stats = [&](float x0, float x1, float x2, float x3, float x4, float x5, float x6, float x7, bool first,
+                   int c) {
+    const float d0 = x0 - x4, d1 = x1 - x5;
+    const float d2 = x2 - x6, d3 = x3 - x7;
+    float ah = acc_hi[c];
+    ah = fmaf(d0, d0, ah); ah = fmaf(d1, d1, ah); ah = fmaf(d2, d2, ah); ah = fmaf(d3, d3, ah);
+    acc_hi[c] = ah;
+    const float u0 = x0 + x4, u1 = x1 + x5;
+    const float u2 = x2 + x6, u3 = x3 + x7;
+    const float a0 = u0 + u1, a1 = u0 - u1, a2 = u2 + u3, a3 = u2 - u3;
+    const float y0 = a0 + a2, y2 = a0 - a2;
+    float am = acc_mid[c], am2 = acc_mid2[c];
+    am2 = fmaf(a1, a1, am2); am2 = fmaf(a3, a3, am2); am = fmaf(y2, y2, am);
+    acc_mid[c] = am; acc_mid2[c] = am2;
+    if (first) {
+      piv[c] = y0;
+    } else {
+      const float dv = y0 - piv[c];
+      ssum[c] += dv;
+      ssq[c] = fmaf(dv, dv, ssq[c]);
+    }
+  };
+
+  // With logits: column c's statistics and the rows' partial dot products
+  // with the queries (value index k * NQL + g), column by column so that
+  // only eight widened values are live next to the partial sums.
+  auto column = [&](const uint4 (&r)[8], bool first, int c, float* part) {
+    float x[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) E::unpack(r[k], x[k]);
+    for (int k = 0; k < 8; ++k) x[k] = E::get(r[k], c);
+    stats(x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7], first, c);
+    if constexpr (NQL > 0 && !DOT2) {
 #pragma unroll
-    for (int c = 0; c < VEC; ++c) {
-      const float d0 = x[0][c] - x[4][c], d1 = x[1][c] - x[5][c];
-      const float d2 = x[2][c] - x[6][c], d3 = x[3][c] - x[7][c];
-      float ah = acc_hi[c];
-      ah = fmaf(d0, d0, ah); ah = fmaf(d1, d1, ah); ah = fmaf(d2, d2, ah); ah = fmaf(d3, d3, ah);
-      acc_hi[c] = ah;
-      const float u0 = x[0][c] + x[4][c], u1 = x[1][c] + x[5][c];
-      const float u2 = x[2][c] + x[6][c], u3 = x[3][c] + x[7][c];
-      const float a0 = u0 + u1, a1 = u0 - u1, a2 = u2 + u3, a3 = u2 - u3;
-      const float y0 = a0 + a2, y2 = a0 - a2;
-      float am = acc_mid[c], am2 = acc_mid2[c];
-      am2 = fmaf(a1, a1, am2); am2 = fmaf(a3, a3, am2); am = fmaf(y2, y2, am);
-      acc_mid[c] = am; acc_mid2[c] = am2;
-      if (first) {
-        piv[c] = y0;
+      for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int g = 0; g < NQL; ++g) part[k * NQL + g] = fmaf(lq[g][c], x[k], part[k * NQL + g]);
+    }
+  };
+
+  auto consume = [&](const uint4 (&r)[8], bool first, int l) {
+    constexpr int V = NQL > 0 ? 8 * NQL : 1;
+    float part[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) part[i] = 0.f;
+    if constexpr (NQL == 0 || DOT2) {
+      if constexpr (DOT2) {
+        // Packed dot products of the raw key words (two columns each).
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+#pragma unroll
+          for (int w = 0; w < VEC / 2; ++w)
+#pragma unroll
+            for (int g = 0; g < NQL; ++g) part[k * NQL + g] = dot2_acc<DT>(word_of(r[k], w), lqw[g][w], part[k * NQL + g]);
+      }
+      // Statistics: widen the eight rows at once.
+      float x[8][VEC];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) E::unpack(r[k], x[k]);
+#pragma unroll
+      for (int c = 0; c < VEC; ++c)
+        stats(x[0][c], x[1][c], x[2][c], x[3][c], x[4][c], x[5][c], x[6][c], x[7][c], first, c);
+    } else {
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) column(r, first, c, part);
+    }
+    if constexpr (NQL > 0) {
+      if constexpr (DOT2) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) part[i] *= p.logit_scale;
+      }
+      // Sum each row's partial dots over its LPR lanes, then stage them.
+      Butterfly<V, V, LPR / 2, LPR>::run(part, cc);
+      if constexpr (V >= LPR) {
+        constexpr int PER_LANE = V / LPR;
+#pragma unroll
+        for (int u = 0; u < PER_LANE; ++u) {
+          const int idx = cc * PER_LANE + u;
+          s_lg[(64 * (idx / NQL) + l) * NQL + idx % NQL] = part[u];
+        }
       } else {
-        const float dv = y0 - piv[c];
-        ssum[c] += dv;
-        ssq[c] = fmaf(dv, dv, ssq[c]);
+        // REP = LPR / V lanes hold each complete sum; all of them store it
+        // (same address, same value), which keeps the loop free of branches.
+        constexpr int REP = LPR / V;
+        const int idx = cc / REP;
+        s_lg[(64 * (idx / NQL) + l) * NQL + idx % NQL] = part[0];
       }
     }
   };
 
   uint4 ra[8], rb[8];
-  load_rows<DT, LPR>(base, row_bytes, slot, ra);
+  load_rows(tbase, stride64, lane_off(slot), ra);
+  int seg = 0;
+  if constexpr (NQL > 0) {
+    // The logits need this block's queries before the first rows arrive: in
+    // a ragged batch, find the segment now (s_cu was requested above).
+    if (need_seg) {
+      __syncthreads();
+      seg = find_segment(s_cu, p.num_segments, gb);
+    }
+#pragma unroll
+    for (int g = 0; g < NQL; ++g) {
+      const int qc = min(g, nq - 1);
+      const int st = qc / p.group, gg = qc - st * p.group;
+      const char* qp = reinterpret_cast<const char*>(p.q) +
+                       ((int64_t)seg * p.q_seg_stride + (int64_t)st * p.q_tok_stride +
+                        (int64_t)(h * p.group + gg) * p.q_head_stride + (int64_t)cc * VEC) * QSZ;
+      if constexpr (DOT2) {
+        const uint4 w = ld16(qp);
+#pragma unroll
+        for (int i = 0; i < VEC / 2; ++i) lqw[g][i] = g < nq ? word_of(w, i) : 0u;
+      } else {
+        const float sc = g < nq ? p.logit_scale : 0.f;
+#pragma unroll
+        for (int e0 = 0; e0 < VEC; e0 += EQ::VEC) {
+          float tmp[EQ::VEC];
+          EQ::unpack(ld16(qp + e0 * QSZ), tmp);
+#pragma unroll
+          for (int e = 0; e < EQ::VEC && e0 + e < VEC; ++e) lq[g][e0 + e] = tmp[e] * sc;
+        }
+      }
+    }
+  }
 #pragma unroll
   for (int j = 0; j < NLO; j += 2) {
-    load_rows<DT, LPR>(base, row_bytes, slot + NSLOT * (j + 1), rb);
-    consume(ra, j == 0);
-    if (j + 2 < NLO) load_rows<DT, LPR>(base, row_bytes, slot + NSLOT * (j + 2), ra);
-    consume(rb, false);
+    load_rows(tbase, stride64, lane_off(slot + NSLOT * (j + 1)), rb);
+    consume(ra, j == 0, slot + NSLOT * j);
+    if (j + 2 < NLO) load_rows(tbase, stride64, lane_off(slot + NSLOT * (j + 2)), ra);
+    consume(rb, false, slot + NSLOT * (j + 1));
   }
 
   float hi = 0.f, mid = 0.f;
@@ -147,6 +284,14 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
     s_m2[slot * D + cc * VEC + c] = m2_t;
   }
   __syncthreads();
+
+  if constexpr (NQL > 0) {
+    // The tile's logits: 512 x NQL fp32, contiguous, 16 bytes per thread.
+    float* dst = p.logits + (int64_t)tile * kBlock * NQL;
+#pragma unroll
+    for (int i = 4 * t; i < kBlock * NQL; i += 4 * 256)
+      *reinterpret_cast<float4*>(dst + i) = *reinterpret_cast<const float4*>(s_lg + i);
+  }
 
   // Per column: merge the NSLOT partial (mean, M2) pairs (equal counts NLO).
   float elow = 0.f;
@@ -189,16 +334,10 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreParams p) {
 
   // Inline query-aware bound: tau_j = q.kbar/sqrt(d) + ||q|| sqrt(E_AC)/sqrt(d),
   // max over the segment's queries of every query head sharing kv head h.
-  int seg = 0;
-  if (need_seg) {
+  if (NQL == 0 && need_seg) {
     // s_cu was filled before the key stream; block_sum's barriers have
-    // made it visible.  Binary search for the segment holding block gb.
-    int lo = 0, hi = p.num_segments - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_cu[mid] <= gb) lo = mid; else hi = mid - 1;
-    }
-    seg = lo;
+    // made it visible.
+    seg = find_segment(s_cu, p.num_segments, gb);
   }
   if (want_bound) {
     const float sqrt_d = sqrtf((float)D);
@@ -481,19 +620,32 @@ __global__ __launch_bounds__(256) void block_energy_kernel(EnergyParams p) {
 // ---------------------------------------------------------------- launchers
 namespace oc {
 
+template <int DT, int LPR, int QDT>
+static hipError_t launch_score_q(const ScoreParams& p, hipStream_t s) {
+  const int tiles = p.total_blocks * p.num_kv_heads;
+  if (!p.logits) {
+    hipLaunchKernelGGL((score_kernel<DT, LPR, QDT, 0>), dim3(tiles), dim3(256), 0, s, p);
+    return hipGetLastError();
+  }
+  // Logits: lanes per row of the attention's value loads (LPR <= 64).
+  if constexpr (LPR <= 64) {
+    switch (logits_nq_pad(p.sq * p.group)) {
+      case 1: hipLaunchKernelGGL((score_kernel<DT, LPR, QDT, 1>), dim3(tiles), dim3(256), 0, s, p); break;
+      case 2: hipLaunchKernelGGL((score_kernel<DT, LPR, QDT, 2>), dim3(tiles), dim3(256), 0, s, p); break;
+      default: hipLaunchKernelGGL((score_kernel<DT, LPR, QDT, 4>), dim3(tiles), dim3(256), 0, s, p); break;
+    }
+    return hipGetLastError();
+  }
+  return hipErrorInvalidValue;
+}
+
 template <int DT, int LPR>
 static hipError_t launch_score_t(const ScoreParams& p, hipStream_t s) {
-  const int tiles = p.total_blocks * p.num_kv_heads;
   // Without queries the query type is irrelevant: use the key type.
   const int qdt = p.q ? p.q_dtype : DT;
-  if (qdt == DT) {
-    hipLaunchKernelGGL((score_kernel<DT, LPR, DT>), dim3(tiles), dim3(256), 0, s, p);
-  } else if (qdt == kF32) {
-    hipLaunchKernelGGL((score_kernel<DT, LPR, kF32>), dim3(tiles), dim3(256), 0, s, p);
-  } else {
-    return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  if (qdt == DT) return launch_score_q<DT, LPR, DT>(p, s);
+  if (qdt == kF32) return launch_score_q<DT, LPR, kF32>(p, s);
+  return hipErrorInvalidValue;
 }
 
 template <int DT>
@@ -515,6 +667,13 @@ bool score_supported(int dt, int head_dim) {
   if (head_dim % vec) return false;
   const int lpr = head_dim / vec;
   return lpr == 8 || lpr == 16 || lpr == 32 || lpr == 64 || lpr == 128;
+}
+
+// True when score_kernel can also write the attention logits of nq query
+// rows per kv head.
+bool score_logits_supported(int dt, int head_dim, int nq) {
+  const int vec = (dt == kF32) ? 4 : 8;
+  return score_supported(dt, head_dim) && head_dim / vec <= 64 && nq >= 1 && nq <= kLogitsMaxQ;
 }
 
 hipError_t launch_score(const ScoreParams& p, hipStream_t s) {

@@ -1,0 +1,168 @@
+"""GPU parity: attention logits formed in the scoring pass.
+
+The scoring kernel can write q.k * log2(e)/sqrt(d) for every key row while it
+streams the keys (at most 4 query rows per kv head); the decode attention then
+reads those logits and the values instead of keys and values.  Checked here:
+the logits against the float64 oracle (``block_logits``), the scores of the
+same launch bit for bit against a launch without logits, and the attention
+from logits against the oracle and against the key-reading attention.
+Tolerances: logits 1e-5 of the largest |logit|; attention as in
+test_gpu_attention.py (1e-4 fp32 inputs, 2e-3 bf16/fp16 inputs, fp32 out).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oc_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+LOG2E = 1.0 / math.log(2.0)
+
+
+def np32(t):
+    return t.detach().float().cpu().numpy()
+
+
+def close(out, ref, rel):
+    out = np.asarray(out, np.float64)
+    ref = np.asarray(ref, np.float64)
+    scale = max(np.abs(ref).max(), 1e-6)
+    err = np.abs(out - ref).max() / scale
+    assert err <= rel, f"max error {err:.3e} relative to scale (tolerance {rel})"
+
+
+def make(dev, nb, sq, hq, hkv, d, dtype, seed):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    q = torch.randn(sq, hq, d, generator=g, device=dev).to(dtype)
+    k = (torch.randn(nb * 512, hkv, d, generator=g, device=dev) + 0.5).to(dtype)
+    v = torch.randn(nb * 512, hkv, d, generator=g, device=dev).to(dtype)
+    return q, k, v
+
+
+CASES = [
+    # (sq, hq, hkv, d, dtype): nq = sq * hq / hkv query rows per kv head
+    (1, 32, 16, 256, torch.bfloat16),   # C2 shape (nq 2)
+    (1, 32, 8, 128, torch.bfloat16),    # C3 shape (nq 4)
+    (1, 1, 1, 128, torch.bfloat16),     # C1 shape (nq 1)
+    (1, 6, 2, 64, torch.bfloat16),      # nq 3 (padded to 4)
+    (2, 2, 2, 128, torch.float32),      # two query tokens, nq 2
+    (1, 4, 4, 256, torch.float32),      # fp32 keys, 64 lanes per row
+    (1, 8, 2, 128, torch.float16),      # fp16, nq 4
+    (1, 2, 2, 512, torch.bfloat16),     # 64 lanes per row, bf16
+]
+
+
+@pytest.mark.parametrize("sq,hq,hkv,d,dtype", CASES)
+def test_score_logits_vs_oracle(dev, sq, hq, hkv, d, dtype):
+    from orthocache_amd import _ops
+
+    nb = 3
+    q, k, v = make(dev, nb, sq, hq, hkv, d, dtype, seed=d + hq + sq)
+    nq = sq * hq // hkv
+    with_lg = _ops.score(k, q, want_logits=True)
+    plain = _ops.score(k, q)
+    torch.cuda.synchronize()
+    lg = np32(with_lg.logits)
+    nqp = _ops.logits_nq_pad(nq)
+    assert lg.shape == (nb, hkv, 512, nqp)
+    ref = O.block_logits(np32(q), np32(k)) * LOG2E
+    close(lg[..., :nq], ref, 1e-5)
+    assert np.all(lg[..., nq:] == 0.0)
+    # The scores of the launch that also writes logits are the same bits.
+    assert torch.equal(with_lg.zeta, plain.zeta)
+    assert torch.equal(with_lg.tau_max, plain.tau_max)
+
+
+def test_score_logits_segments_and_pages(dev):
+    from orthocache_amd import _ops
+
+    # Three segments of 2, 1 and 3 blocks in a shuffled page pool.
+    hkv, g, d = 4, 2, 128
+    seg_blocks = [2, 1, 3]
+    nb = sum(seg_blocks)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    pool = torch.randn(nb * 512, hkv, d, generator=gen, device=dev).to(torch.bfloat16)
+    q = torch.randn(3, 1, hkv * g, d, generator=gen, device=dev).to(torch.bfloat16)
+    pages = torch.tensor([4, 0, 5, 2, 1, 3], dtype=torch.int32, device=dev)
+    cu = torch.tensor([0, 2, 3, 6], dtype=torch.int32, device=dev)
+    res = _ops.score(pool, q, cu_blocks=cu, num_segments=3, pages=pages, want_logits=True)
+    torch.cuda.synchronize()
+    lg = np32(res.logits)
+    poolf, qf, pg = np32(pool), np32(q), pages.cpu().numpy()
+    j = 0
+    for s, n in enumerate(seg_blocks):
+        keys = np.concatenate([poolf[pg[b] * 512:(pg[b] + 1) * 512] for b in range(j, j + n)])
+        ref = O.block_logits(qf[s], keys) * LOG2E
+        close(lg[j:j + n, ..., :g], ref, 1e-5)
+        j += n
+
+
+def test_logits_limits(dev):
+    from orthocache_amd import _ops
+
+    q, k, _ = make(dev, 1, 1, 10, 2, 128, torch.bfloat16, seed=1)  # nq 5
+    with pytest.raises(ValueError):
+        _ops.score(k, q, want_logits=True)
+
+
+@pytest.mark.parametrize("sq,hq,hkv,d,dtype", CASES)
+def test_attend_from_logits(dev, sq, hq, hkv, d, dtype):
+    from orthocache_amd import _ops
+
+    nb = 5
+    q, k, v = make(dev, nb, sq, hq, hkv, d, dtype, seed=3 * d + hq)
+    sc = _ops.score(k, q, want_logits=True)
+    mask = torch.tensor([1, 0, 1, 1, 0], dtype=torch.bool, device=dev)
+    c = _ops.mask_compact(num_blocks=nb, num_kv_heads=hkv, device=dev, mask_in=mask)
+    out_lg = _ops.attend(q, k, v, c.indices, c.num_active, out_dtype=torch.float32, logits=sc.logits)
+    out_k = _ops.attend(q, k, v, c.indices, c.num_active, out_dtype=torch.float32)
+    ref = O.attention_active_blocks(np32(q), np32(k), np32(v), [0, 2, 3])
+    tol = 1e-4 if dtype == torch.float32 else 2e-3
+    close(np32(out_lg), ref, tol)
+    close(np32(out_lg), np32(out_k), 1e-5)
+
+
+def test_attend_from_logits_per_head_and_empty(dev):
+    from orthocache_amd import _ops
+
+    nb, hkv = 4, 2
+    q, k, v = make(dev, nb, 1, 4, hkv, 128, torch.bfloat16, seed=9)
+    sc = _ops.score(k, q, want_logits=True)
+    # head 0 keeps blocks 1 and 3; head 1 keeps nothing (gated kernel: zeros)
+    m = torch.tensor([[0, 0], [1, 0], [0, 0], [1, 0]], dtype=torch.bool, device=dev)
+    c = _ops.mask_compact(num_blocks=nb, num_kv_heads=hkv, device=dev, mask_in=m, want_indices=False,
+                          want_head_lists=True)
+    out = _ops.attend(q, k, v, c.head_indices, c.head_num_active, per_head=True, out_dtype=torch.float32,
+                      logits=sc.logits)
+    ref = O.attention_per_head_gated(np32(q), np32(k), np32(v), m.cpu().numpy())
+    close(np32(out), ref, 2e-3)
+    assert np.all(np32(out)[:, 2:] == 0)
+
+
+def test_decode_layer_uses_logits_and_matches(dev):
+    """The fused layer (scoring-pass logits for nq <= 4) against the three
+    separate calls without logits: same mask and permutation bit for bit,
+    attention within fp32 rounding."""
+    from orthocache_amd import _ops, workloads
+
+    nb, hkv, hq, d = 16, 4, 8, 256
+    k = workloads.make_keys(nb, hkv, d, seed=31, device=dev, noise_blocks=2)
+    v = workloads.make_values(nb * 512, hkv, d, seed=32, device=dev)
+    q = workloads.make_queries((1, hq, d), d, seed=33, device=dev)
+    assert _ops.layer_uses_logits(k.dtype, d, hq // hkv)
+    sc = _ops.score(k, q)
+    tau, zmax = workloads.calibrate_unified(sc.tau_max[0], sc.zeta, evict=0.75)
+    layer = _ops.DecodeLayer(q, k, v, tau, zmax, out_dtype=torch.float32)
+    out = layer.run()
+    c = _ops.mask_compact(num_blocks=nb, num_kv_heads=hkv, device=dev, tau_max=sc.tau_max, zeta=sc.zeta,
+                          tau=tau, zeta_max=zmax)
+    ref = _ops.attend(q, k, v, c.indices, c.num_active, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(layer.indices, c.indices) and torch.equal(layer.num_active, c.num_active)
+    close(np32(out), np32(ref), 1e-5)

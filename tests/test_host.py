@@ -48,7 +48,7 @@ def test_binding_covers_header(lib):
 
 
 def test_abi_version(lib):
-    assert lib.oc_abi_version() == 2
+    assert lib.oc_abi_version() == 3
 
 
 def test_struct_sizes_match_header_layout(lib):

@@ -294,6 +294,56 @@ class TestAttention:
         assert np.all(gated[:, 1] == 0)
 
 
+class TestBlockLogits:
+    def _softmax_attend(self, lg, v, blocks, hkv, g):
+        # lg: (nb, Hkv, 512, Sq*G) logits; softmax over the retained tokens, times V.
+        d = v.shape[-1]
+        nq = lg.shape[-1]
+        sq = nq // g
+        out = np.zeros((sq, hkv * g, d))
+        tok = np.concatenate([np.arange(b * 512, (b + 1) * 512) for b in blocks])
+        for h in range(hkv):
+            l_h = np.concatenate([lg[b, h] for b in blocks], axis=0)  # (T, Sq*G)
+            w = np.exp(l_h - l_h.max(0, keepdims=True))
+            w /= w.sum(0, keepdims=True)
+            o = w.T @ v[tok, h]                                        # (Sq*G, D)
+            for i in range(nq):
+                t, gg = divmod(i, g)
+                out[t, h * g + gg] = o[i]
+        return out
+
+    def test_softmax_of_logits_reproduces_attention(self):
+        rng = np.random.default_rng(21)
+        q = rng.standard_normal((3, 4, 16))
+        k = rng.standard_normal((4 * 512, 2, 16))
+        v = rng.standard_normal((4 * 512, 2, 16))
+        lg = O.block_logits(q, k)
+        assert lg.shape == (4, 2, 512, 6)
+        blocks = [0, 2, 3]
+        np.testing.assert_allclose(self._softmax_attend(lg, v, blocks, 2, 2),
+                                   O.attention_active_blocks(q, k, v, blocks), rtol=1e-10, atol=1e-12)
+
+    def test_self_logit_known_answer(self):
+        rng = np.random.default_rng(22)
+        q = rng.standard_normal((1, 1, 64))
+        k = rng.standard_normal((512, 1, 64))
+        k[37, 0] = q[0, 0]
+        lg = O.block_logits(q, k)
+        assert np.isclose(lg[0, 0, 37, 0], (q[0, 0] ** 2).sum() / 8.0)
+
+    def test_planted_gqa_fold_mistake_fails(self):
+        # Query heads grouped the wrong way round (h + g*Hkv instead of h*G + g)
+        # must not reproduce the attention.
+        rng = np.random.default_rng(23)
+        q = rng.standard_normal((1, 4, 8))
+        k = rng.standard_normal((2 * 512, 2, 8))
+        v = rng.standard_normal((2 * 512, 2, 8))
+        bad_q = q[:, [0, 2, 1, 3]]
+        lg_bad = O.block_logits(bad_q, k)
+        assert not np.allclose(self._softmax_attend(lg_bad, v, [0, 1], 2, 2),
+                               O.attention_active_blocks(q, k, v, [0, 1]))
+
+
 class TestPlantedMistakes:
     """Each plants a plausible oracle mistake and checks that a pin above catches it."""
 
