@@ -29,10 +29,12 @@
  *    pool size in pages; page numbers outside [0, num_pages) are clamped into
  *    it (the kernels never read outside the pool), as are block-list entries
  *    outside their segment.  (ABI version 2 appended these fields.)
- *  - Scoring-pass logits (ABI version 3 appended `logits` to oc_score_args
- *    and oc_attend_args): with at most 4 query rows per kv head, the scoring
+ *  - ABI version 3 appended to oc_score_args and oc_attend_args:
+ *    scoring-pass logits (with at most 4 query rows per kv head the scoring
  *    pass can also write the attention logits of every key row it streams,
- *    and the decode attention can read them instead of the keys.
+ *    and the decode attention can read them instead of the keys), and the
+ *    two-gate mask written by the scoring pass, which the decode attention
+ *    of one segment can take instead of a compacted list.
  */
 #ifndef ORTHOCACHE_HIP_H
 #define ORTHOCACHE_HIP_H
@@ -113,7 +115,13 @@ int oc_block_energy(const void* keys, int32_t keys_dtype, int64_t tok_stride, in
  * row i = t*group + g of kv head h (zero for i >= sq*group).  The logits of
  * softmax(q.k / sqrt(d)) (src/orthocache/adaptive_attention.py:60-61, :103-104) in the
  * base-2 form, formed while the keys stream so that oc_attend need not read
- * the keys again.  No counterpart in the reference. */
+ * the keys again.  No counterpart in the reference.
+ * mask (optional, needs q and tau_max): the two-gate mask of each (block, kv
+ * head), (tau_max >= tau) & (zeta <= zeta_max) in fp32 with NaN -> 0, as
+ * uint8 (total_blocks, Hkv) -- compute_multiband_mask
+ * (src/orthocache/spectral_energy.py:199-234) from the same scores, with
+ * per-segment thresholds tau_arr / zeta_max_arr when given (as in
+ * oc_mask_compact). */
 typedef struct oc_score_args {
   const void* keys;
   int32_t keys_dtype;
@@ -135,6 +143,11 @@ typedef struct oc_score_args {
   const int32_t* pages; /* (total_blocks) physical page per block, or NULL */
   int32_t num_pages;    /* pages in the key pool (used when pages != NULL) */
   float* logits;        /* (total_blocks, Hkv, 512, nq_pad), or NULL (ABI 3) */
+  uint8_t* mask;        /* (total_blocks, Hkv) two-gate mask, or NULL (ABI 3) */
+  const float* tau_arr; /* device, per segment, or NULL -> tau (ABI 3) */
+  float tau;
+  const float* zeta_max_arr;
+  float zeta_max;
 } oc_score_args;
 int oc_score_blocks(const oc_score_args* a, void* stream);
 
@@ -218,6 +231,13 @@ int oc_copy_blocks(const void* src, void* dst, const int32_t* indices, const int
  * logits (ABI 3, optional): the oc_score_blocks logits of the same q, keys
  * and segments; the decode kernel then reads them and the values only (k may
  * be NULL).  Needs block_size 512 and 1 <= sq*group <= 4.
+ * mask (ABI 3, optional): a (total_blocks, Hkv) uint8 block mask of one
+ * segment (cu_blocks NULL, per_head 0, 1 <= total_blocks <= 2048, decode
+ * family) instead of indices/counts, which are then ignored: the attention
+ * takes the blocks kept by any head (the unified list of
+ * orthocache_attention, src/orthocache/adaptive_attention.py:29-40) and
+ * writes the active-first permutation to indices_out and the count to
+ * num_active_out (both required), as oc_mask_compact would.
  * workspace >= oc_attend_workspace_size(...). */
 typedef struct oc_attend_args {
   const void* q;
@@ -241,6 +261,9 @@ typedef struct oc_attend_args {
   const int32_t* pages;    /* (total_blocks) physical page per block, or NULL */
   int32_t num_pages;       /* pages in the key/value pools (used when pages != NULL) */
   const float* logits;     /* scoring-pass logits, or NULL (ABI 3) */
+  const uint8_t* mask;     /* (total_blocks, Hkv) block mask instead of a list, or NULL (ABI 3) */
+  int32_t* indices_out;    /* (total_blocks), written when mask is given */
+  int32_t* num_active_out; /* (1), written when mask is given */
 } oc_attend_args;
 size_t oc_attend_workspace_size(const oc_attend_args* a);
 int oc_attend(const oc_attend_args* a, void* workspace, size_t workspace_bytes, void* stream);
@@ -264,7 +287,9 @@ int oc_attend_plan(const oc_attend_args* a, int32_t* kernel, int32_t* nsplit);
  * stream.  At most 16 queries per kv head (sq * group).  With at most 4
  * (and head_dim / (16 / esize) <= 64) the scoring pass also writes the
  * attention logits into the workspace and the attention reads only the
- * values of the retained blocks.
+ * values of the retained blocks.  For one segment of at most 2048 blocks the
+ * scoring pass also writes the two-gate mask and the attention derives the
+ * list from it (no separate compaction launch); the outputs are the same.
  * workspace >= oc_decode_layer_workspace_size(...). */
 typedef struct oc_layer_args {
   const void* q;

@@ -39,7 +39,8 @@ class ScoreArgs(C.Structure):
                 ("q", _vp), ("q_dtype", _i32), ("q_seg_stride", _i64), ("q_tok_stride", _i64),
                 ("q_head_stride", _i64), ("sq", _i32), ("group", _i32),
                 ("tau_max", _vp), ("zeta", _vp), ("dc", _vp), ("e_low", _vp), ("e_mid", _vp),
-                ("e_high", _vp), ("e_ac", _vp), ("pages", _vp), ("num_pages", _i32), ("logits", _vp)]
+                ("e_high", _vp), ("e_ac", _vp), ("pages", _vp), ("num_pages", _i32), ("logits", _vp),
+                ("mask", _vp), ("tau_arr", _vp), ("tau", _f32), ("zeta_max_arr", _vp), ("zeta_max", _f32)]
 
 
 class BoundArgs(C.Structure):
@@ -71,7 +72,7 @@ class AttendArgs(C.Structure):
                 ("indices", _vp), ("counts", _vp), ("per_head", _i32), ("uniform", _vp),
                 ("out", _vp), ("out_dtype", _i32),
                 ("out_seg_stride", _i64), ("out_tok_stride", _i64), ("out_head_stride", _i64), ("pages", _vp), ("num_pages", _i32),
-                ("logits", _vp)]
+                ("logits", _vp), ("mask", _vp), ("indices_out", _vp), ("num_active_out", _vp)]
 
 
 class LayerArgs(C.Structure):

@@ -91,6 +91,7 @@ class Scores:
     e_ac: torch.Tensor | None = None
     bounds: torch.Tensor | None = None  # (Sq*G, nb, Hkv)
     logits: torch.Tensor | None = None  # (nb, Hkv, 512, nq_pad): q.k * log2(e)/sqrt(d)
+    mask: torch.Tensor | None = None    # (nb, Hkv) bool: the two-gate mask
 
 
 INLINE_QUERY_LIMIT = 16
@@ -100,6 +101,33 @@ LOGITS_QUERY_LIMIT = 4  # query rows per kv head for scoring-pass logits
 def logits_nq_pad(nq: int) -> int:
     """Query slots per key row in the scoring-pass logits (1, 2 or 4)."""
     return 1 if nq <= 1 else (2 if nq <= 2 else 4)
+
+
+MASK_LIST_MAX_BLOCKS = 2048  # blocks of one segment whose attention can take a mask
+
+
+def layer_uses_keep(num_blocks: int, single_segment: bool) -> bool:
+    """Whether oc_decode_layer has its scoring pass write the two-gate mask
+    and the attention derive the list from it (the library's
+    layer_uses_keep): one segment of 1..2048 blocks."""
+    return single_segment and 1 <= num_blocks <= MASK_LIST_MAX_BLOCKS
+
+
+def _set_thresholds(a, tau, zeta_max, device):
+    """tau / zeta_max (Python floats, rounded to fp32, or per-segment device
+    tensors) into an argument struct; returns tensors to keep alive."""
+    keep = []
+    if isinstance(tau, torch.Tensor):
+        t = tau.to(device=device, dtype=torch.float32).contiguous()
+        a.tau_arr = ptr(t); keep.append(t)
+    else:
+        a.tau = float(tau)
+    if isinstance(zeta_max, torch.Tensor):
+        z = zeta_max.to(device=device, dtype=torch.float32).contiguous()
+        a.zeta_max_arr = ptr(z); keep.append(z)
+    else:
+        a.zeta_max = float(zeta_max)
+    return keep
 
 
 def layer_uses_logits(kv_dtype: torch.dtype, head_dim: int, nq: int) -> bool:
@@ -112,14 +140,17 @@ def layer_uses_logits(kv_dtype: torch.dtype, head_dim: int, nq: int) -> bool:
 
 def score(keys: torch.Tensor, q: torch.Tensor | None = None, *, want_bands: bool = False,
           want_bounds: bool = False, want_zeta: bool = True, cu_blocks: torch.Tensor | None = None,
-          num_segments: int = 1, pages: torch.Tensor | None = None, want_logits: bool = False) -> Scores:
+          num_segments: int = 1, pages: torch.Tensor | None = None, want_logits: bool = False,
+          gate=None) -> Scores:
     """One pass over the keys: zeta, bands and (with q) the query-aware bound.
 
     keys: (S, Hkv, D), S a multiple of 512.  q: (Sq, Hq, D) for one segment or
     (B, Sq, Hq, D) with cu_blocks for several.  Small query counts get their
     maximum bound inline; large ones (or want_bounds) go through the tiled
     bound kernel.  want_logits (at most 4 query rows per kv head): also the
-    attention logits of every key row, formed in the same pass.
+    attention logits of every key row, formed in the same pass.  gate =
+    (tau, zeta_max): also the two-gate mask from the same scores (inline
+    bound only).
     """
     require_gpu(keys, q, cu_blocks)
     keys = _kv_view(keys, "keys")
@@ -168,6 +199,8 @@ def score(keys: torch.Tensor, q: torch.Tensor | None = None, *, want_bands: bool
         if not (inline and 1 <= nq <= LOGITS_QUERY_LIMIT):
             raise ValueError(f"logits need 1..{LOGITS_QUERY_LIMIT} query rows per kv head, got {nq}")
         res.logits = torch.empty((nb, hkv, BLOCK, logits_nq_pad(nq)), **f32)
+    if gate is not None and not inline:
+        raise ValueError("the two-gate mask from the scoring pass needs the inline bound (at most 16 query rows)")
     a = N.ScoreArgs()
     a.keys = ptr(keys); a.keys_dtype = dtype_code(keys.dtype)
     a.keys_tok_stride = keys.stride(0); a.keys_head_stride = keys.stride(1)
@@ -184,7 +217,15 @@ def score(keys: torch.Tensor, q: torch.Tensor | None = None, *, want_bands: bool
     a.zeta = ptr(res.zeta); a.dc = ptr(res.dc); a.e_low = ptr(res.e_low); a.e_mid = ptr(res.e_mid)
     a.e_high = ptr(res.e_high); a.e_ac = ptr(res.e_ac)
     a.logits = ptr(res.logits)
+    alive = []
+    if gate is not None:
+        res.mask = torch.empty(tiles, dtype=torch.uint8, device=dev)
+        a.mask = ptr(res.mask)
+        alive = _set_thresholds(a, gate[0], gate[1], dev)
     check(lib().oc_score_blocks(C.byref(a), stream_ptr(dev)), "oc_score_blocks")
+    del alive
+    if res.mask is not None:
+        res.mask = res.mask.view(torch.bool)
     if q_ok and not inline:
         if cu_blocks is not None:
             raise ValueError("many-query bounds need a single segment")
@@ -310,14 +351,27 @@ def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, indices: torch.Ten
            block_size: int = BLOCK, per_head: bool = False, uniform: torch.Tensor | None = None,
            out_dtype: torch.dtype | None = None, cu_blocks: torch.Tensor | None = None,
            num_segments: int = 1, out: torch.Tensor | None = None, pages: torch.Tensor | None = None,
-           logits: torch.Tensor | None = None) -> torch.Tensor:
+           logits: torch.Tensor | None = None, mask: torch.Tensor | None = None,
+           indices_out: torch.Tensor | None = None, num_active_out: torch.Tensor | None = None) -> torch.Tensor:
     """Attention over the listed blocks.  q: (Sq, Hq, D) (or (B, Sq, Hq, D) with
     cu_blocks); k, v: (S, Hkv, D).  Returns q-shaped output in out_dtype.
     logits: the ``score(..., want_logits=True)`` logits of the same q and keys;
-    the keys are then not read."""
+    the keys are then not read.  mask: a (nb, Hkv) block mask of one segment
+    instead of indices/counts (pass None for those); the kernel takes the
+    blocks any head keeps and writes the active-first permutation and the
+    count into indices_out / num_active_out when given."""
     a, out, q = _attend_args(q, k, v, indices, counts, block_size=block_size, per_head=per_head, uniform=uniform,
                              out_dtype=out_dtype, cu_blocks=cu_blocks, num_segments=num_segments, out=out,
                              pages=pages)
+    if mask is not None:
+        if mask.dim() != 2 or mask.shape != (a.total_blocks, a.num_kv_heads):
+            raise ValueError(f"mask must be (num_blocks, kv_heads) = ({a.total_blocks}, {a.num_kv_heads})")
+        mask = (mask if mask.dtype == torch.bool else mask != 0).contiguous().view(torch.uint8)
+        if indices_out is None:
+            indices_out = torch.empty((a.total_blocks,), dtype=torch.int32, device=q.device)
+        if num_active_out is None:
+            num_active_out = torch.empty((1,), dtype=torch.int32, device=q.device)
+        a.mask = ptr(mask); a.indices_out = ptr(indices_out); a.num_active_out = ptr(num_active_out)
     if logits is not None:
         if logits.dtype != torch.float32 or not logits.is_contiguous() or logits.shape[:3] != (a.total_blocks, a.num_kv_heads, BLOCK):
             raise ValueError("logits must be the contiguous fp32 (blocks, kv_heads, 512, nq_pad) output of score()")
@@ -345,6 +399,10 @@ def attend_plan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, indices: torc
 def _attend_args(q, k, v, indices, counts, *, block_size: int = BLOCK, per_head: bool = False,
                  uniform=None, out_dtype=None, cu_blocks=None, num_segments: int = 1, out=None, pages=None):
     require_gpu(q, k, v, indices, counts)
+    if indices is None and counts is None:
+        pass  # a block mask replaces the list (attend(..., mask=...))
+    elif indices is None or counts is None:
+        raise ValueError("indices and counts go together")
     out_dtype = out_dtype or q.dtype
     k = _kv_view(k, "keys")
     v = _kv_view(v, "values")
@@ -463,8 +521,11 @@ class DecodeLayer:
         return self.out
 
     def phases(self):
-        """Callables launching the layer's three phases one at a time on the
-        current stream, with the same arguments as run() (for per-kernel timing)."""
+        """Callables (score, compact, attend) launching the layer's phases one
+        at a time on the current stream, with the kernels run() uses (for
+        per-kernel timing).  compact is None when the layer has no compaction
+        launch (one segment: the scoring pass writes the mask and the
+        attention derives the list from it)."""
         a = self.args
         L = lib()
         sa = N.ScoreArgs()
@@ -495,6 +556,14 @@ class DecodeLayer:
                                              dtype=torch.float32, device=self.device)
             sa.logits = ptr(self._phase_logits)
             ta.logits = ptr(self._phase_logits)
+        keep = layer_uses_keep(a.total_blocks, self.cu_blocks is None)
+        if keep:
+            self._phase_keep = torch.empty((a.total_blocks, a.num_kv_heads), dtype=torch.uint8, device=self.device)
+            sa.mask = ptr(self._phase_keep)
+            sa.tau_arr = a.tau_arr; sa.tau = a.tau; sa.zeta_max_arr = a.zeta_max_arr; sa.zeta_max = a.zeta_max
+            ta.mask = ptr(self._phase_keep)
+            ta.indices = None; ta.counts = None
+            ta.indices_out = a.indices; ta.num_active_out = a.num_active
         ws = int(L.oc_attend_workspace_size(C.byref(ta)))
         self._phase_ws = torch.empty((max(ws, 1),), dtype=torch.uint8, device=self.device)
         self._phase_args = (sa, ca, ta)
@@ -510,7 +579,7 @@ class DecodeLayer:
         def attend():
             check(L.oc_attend(C.byref(ta), wsp, ws, stream_ptr(dev)), "oc_attend")
 
-        return score, compact, attend
+        return score, (None if keep else compact), attend
 
 
 class PrefillLayer:

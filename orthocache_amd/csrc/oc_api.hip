@@ -126,11 +126,14 @@ int oc_score_blocks(const oc_score_args* a, void* stream) {
     rc = check_q16(a->q, a->q_dtype, a->cu_blocks ? a->q_seg_stride : 0, a->q_tok_stride, a->q_head_stride);
     if (rc) return rc;
   }
+  if (a->mask && (!a->q || !a->tau_max))
+    return fail(OC_ERR_INVALID_ARGUMENT, "the two-gate mask needs q and tau_max");
   oc::ScoreParams p{a->keys, a->keys_tok_stride, a->keys_head_stride, a->keys_dtype, a->head_dim,
                     a->num_kv_heads, a->total_blocks, a->cu_blocks, a->cu_blocks ? a->num_segments : 1,
                     a->q, a->q_dtype, a->q_seg_stride, a->q_tok_stride, a->q_head_stride, a->sq, a->group,
                     a->tau_max, a->zeta, a->dc, a->e_low, a->e_mid, a->e_high, a->e_ac, a->pages,
-                    a->num_pages, a->logits, logit_scale_for(a->head_dim)};
+                    a->num_pages, a->logits, logit_scale_for(a->head_dim),
+                    oc::GateParams{a->mask, nullptr, a->tau_arr, a->tau, a->zeta_max_arr, a->zeta_max}};
   return hip_check(oc::launch_score(p, (hipStream_t)stream), "oc_score_blocks");
 }
 
@@ -214,7 +217,21 @@ int make_attend_params(const oc_attend_args* a, oc::AttendParams& p) {
   if (nseg <= 0) return fail(OC_ERR_INVALID_ARGUMENT, "num_segments must be > 0");
   if ((int64_t)nseg * a->num_kv_heads > oc::kMaxLists)
     return fail(OC_ERR_UNSUPPORTED, "segments x kv heads = %lld exceeds %d", (long long)nseg * a->num_kv_heads, oc::kMaxLists);
-  if (!a->indices || !a->counts) return fail(OC_ERR_INVALID_ARGUMENT, "indices/counts are NULL");
+  if (a->mask) {
+    if (a->cu_blocks && a->num_segments != 1)
+      return fail(OC_ERR_UNSUPPORTED, "mask input: one segment only (use oc_mask_compact lists for several)");
+    if (a->per_head || a->uniform) return fail(OC_ERR_UNSUPPORTED, "mask input: unified lists only");
+    if (a->total_blocks < 1 || a->total_blocks > oc::kMaxLists)
+      return fail(OC_ERR_UNSUPPORTED, "mask input: 1..%d blocks, got %d", oc::kMaxLists, a->total_blocks);
+    if (!a->indices_out || !a->num_active_out)
+      return fail(OC_ERR_INVALID_ARGUMENT, "mask input needs indices_out and num_active_out");
+    const int H = a->num_kv_heads;
+    const int al = (H % 16 == 0) ? 16 : ((H % 4 == 0) ? 4 : 1);
+    if ((reinterpret_cast<uintptr_t>(a->mask) % al) != 0)
+      return fail(OC_ERR_INVALID_ARGUMENT, "mask must be %d-byte aligned for %d kv heads", al, H);
+  } else if (!a->indices || !a->counts) {
+    return fail(OC_ERR_INVALID_ARGUMENT, "indices/counts are NULL");
+  }
   if (a->pages && a->num_pages <= 0) return fail(OC_ERR_INVALID_ARGUMENT, "pages given with num_pages %d", a->num_pages);
   const int chunk = oc::attend_chunk(a->kv_dtype, a->head_dim, a->sq * a->group);
   p = oc::AttendParams{};
@@ -234,9 +251,19 @@ int make_attend_params(const oc_attend_args* a, oc::AttendParams& p) {
   p.out_seg_stride = a->out_seg_stride; p.out_tok_stride = a->out_tok_stride; p.out_head_stride = a->out_head_stride;
   p.pages = a->pages; p.num_pages = a->num_pages;
   p.logits = a->logits;
+  p.keep = a->mask;
+  p.list_out = a->indices_out;
+  p.count_out = a->num_active_out;
+  if (a->mask) {
+    p.indices = a->indices_out;
+    p.counts = a->num_active_out;  // the combine reads the count the attention wrote
+  }
   p.prefill = oc::prefill_supported(a->kv_dtype, a->q_dtype, a->head_dim, a->sq * a->group, a->block_size) ? 1 : 0;
   // The prefill kernel keeps per-thread offsets inside a 64-token tile in 32 bits.
   if (a->k_tok_stride >= (1 << 24) || a->v_tok_stride >= (1 << 24) || a->logits) p.prefill = 0;
+  if (a->mask && p.prefill)
+    return fail(OC_ERR_UNSUPPORTED, "mask input: decode shapes only (%d query rows per kv head take the matrix-core "
+                "kernels; compact with oc_mask_compact)", a->sq * a->group);
   p.nsplit = p.prefill ? oc::prefill_nsplit(p) : 0;
   return OC_OK;
 }
@@ -297,8 +324,15 @@ int oc_attend(const oc_attend_args* a, void* workspace, size_t workspace_bytes, 
 namespace {
 
 struct LayerWs {
-  size_t tau, zeta, idx, cnt, logits, attend, total;
+  size_t tau, zeta, idx, cnt, keep, logits, attend, total;
 };
+
+// True when the layer's scoring pass writes the two-gate keep flags and the
+// attention derives the list from them (one segment of at most kMaxLists
+// blocks): no compaction launch.
+bool layer_uses_keep(const oc_layer_args* a) {
+  return a->cu_blocks == nullptr && a->total_blocks >= 1 && a->total_blocks <= oc::kMaxLists;
+}
 
 // True when the layer's scoring pass also writes the attention logits (the
 // attention then reads values only).
@@ -306,7 +340,7 @@ bool layer_uses_logits(const oc_layer_args* a) {
   return oc::score_logits_supported(a->kv_dtype, a->head_dim, a->sq * a->group);
 }
 
-// Workspace: [tau_max | zeta | indices | num_active | logits | attention partials].
+// Workspace: [tau_max | zeta | indices | num_active | keep | logits | attention partials].
 LayerWs layer_ws_layout(const oc_layer_args* a, size_t attend_bytes, bool logits) {
   LayerWs w{};
   const size_t tiles = (size_t)a->total_blocks * a->num_kv_heads;
@@ -316,6 +350,7 @@ LayerWs layer_ws_layout(const oc_layer_args* a, size_t attend_bytes, bool logits
   w.zeta = off; off += a->zeta ? 0 : align256(tiles * 4);
   w.idx = off; off += a->indices ? 0 : align256((size_t)a->total_blocks * 4);
   w.cnt = off; off += a->num_active ? 0 : align256((size_t)nseg * 4);
+  w.keep = off; off += layer_uses_keep(a) ? align256(tiles) : 0;
   w.logits = off;
   off += logits ? align256(tiles * OC_BLOCK * oc::logits_nq_pad(a->sq * a->group) * sizeof(float)) : 0;
   w.attend = off; off += attend_bytes;
@@ -393,6 +428,11 @@ int decode_layer_impl(const oc_layer_args* a, const oc_block_stats* st, void* wo
   int32_t* idx = a->indices ? a->indices : reinterpret_cast<int32_t*>(ws + w.idx);
   int32_t* cnt = a->num_active ? a->num_active : reinterpret_cast<int32_t*>(ws + w.cnt);
   const hipStream_t s = (hipStream_t)stream;
+  // One segment: the scoring pass writes the keep flags and the attention
+  // derives the list (and writes indices / num_active) itself.
+  const bool use_keep = layer_uses_keep(a);
+  const oc::GateParams gate{use_keep ? reinterpret_cast<uint8_t*>(ws + w.keep) : nullptr, a->mask,
+                            a->tau_arr, a->tau, a->zeta_max_arr, a->zeta_max};
 
   // 1. Scores: from the keys, or bounds from the cached statistics.
   if (st) {
@@ -403,6 +443,8 @@ int decode_layer_impl(const oc_layer_args* a, const oc_block_stats* st, void* wo
     cp.sq = a->sq; cp.group = a->group; cp.head_dim = a->head_dim; cp.num_kv_heads = a->num_kv_heads;
     cp.total_blocks = a->total_blocks; cp.cu_blocks = a->cu_blocks; cp.num_segments = nseg;
     cp.tau_max = tau_max;
+    cp.zeta = st->zeta;
+    if (use_keep) cp.gate = gate;
     rc = hip_check(oc::launch_cached_bound(cp, s), "oc_decode_layer_cached bounds");
     if (rc) return rc;
     zeta_in = st->zeta;
@@ -422,13 +464,18 @@ int decode_layer_impl(const oc_layer_args* a, const oc_block_stats* st, void* wo
       sp.logit_scale = ap.logit_scale;
       ap.logits = sp.logits;
     }
+    if (use_keep) sp.gate = gate;
     rc = hip_check(oc::launch_score(sp, s), "oc_decode_layer scores");
     if (rc) return rc;
     zeta_in = zeta;
   }
 
-  // 2. Mask + compaction.
-  {
+  // 2. Mask + compaction (several segments; one segment takes the keep flags).
+  if (use_keep) {
+    ap.keep = gate.keep;
+    ap.list_out = idx;
+    ap.count_out = cnt;
+  } else {
     oc::CompactParams cp{};
     cp.tau_max = tau_max; cp.tau_parts = 1; cp.zeta = zeta_in;
     cp.tau_arr = a->tau_arr; cp.tau = a->tau; cp.zmax_arr = a->zeta_max_arr; cp.zeta_max = a->zeta_max;

@@ -30,12 +30,20 @@
 // Logits are kept in the log2 domain: s2 = q.k * log2(e) / sqrt(d), weights
 // exp2(s2 - m2); identical to the natural-log form in exact arithmetic.
 //
+// Keep-flag mode (one segment, unified list): instead of a compacted list,
+// the kernel gets the (block, kv head) keep flags of the two-gate mask and
+// every workgroup derives the active list itself -- the OR over heads, a
+// ballot prefix, the list in LDS (one round trip for 1-2 KB of flags, no
+// compaction launch, no dependent load of the count and then the list).
+// Workgroup 0 also writes the active-first permutation and the count, the
+// outputs the compaction would have written.
+//
 // Logits variant (LG): inside the fused decode layer the scoring kernel has
 // already formed every key row's logits while streaming the keys
 // (ScoreParams::logits), so an item reads its rows' logits (NQ floats per
 // row) and the value rows only -- half the bytes of K + V -- and skips the
 // dot products, the butterfly and the LDS logit exchange.
-#include "oc_kernels.h"
+#include "oc_compact_dev.h"
 
 #ifndef OC_ATTEND_THREADS
 #define OC_ATTEND_THREADS 256
@@ -122,6 +130,58 @@ __device__ __forceinline__ int find_list(const int* s_off, int nlists, int item)
   return lo;
 }
 
+// OR of a block's H keep flags (16-, 4- or 1-byte loads, all in flight
+// together).  kp is 16-byte aligned when H is a multiple of 16, 4-byte
+// aligned when H is a multiple of 4.
+__device__ __forceinline__ bool any_flag(const uint8_t* kp, int H) {
+  uint32_t acc = 0;
+  if ((H & 15) == 0) {
+    for (int h = 0; h < H; h += 16) {
+      const uint4 w = *reinterpret_cast<const uint4*>(kp + h);
+      acc |= w.x | w.y | w.z | w.w;
+    }
+  } else if ((H & 3) == 0) {
+    for (int h = 0; h < H; h += 4) acc |= *reinterpret_cast<const uint32_t*>(kp + h);
+  } else {
+    for (int h = 0; h < H; ++h) acc |= kp[h];
+  }
+  return acc != 0;
+}
+
+// The unified active list of one segment from its keep flags, into s_list
+// (ascending block ids); returns the count.  Workgroup 0 also writes the
+// full active-first stable permutation to p.list_out and the count to
+// p.count_out.  s_act holds one flag per block.  Uniform call.
+__device__ int list_from_keep(const AttendParams& p, int* s_list, uint8_t* s_act, int* s_cnt) {
+  const int nb = p.total_blocks, H = p.num_kv_heads;
+  const int t = threadIdx.x;
+  int n = 0;
+  for (int b0 = 0; b0 < nb; b0 += blockDim.x) {
+    const int j = b0 + t;
+    const bool a = j < nb && any_flag(p.keep + (int64_t)j * H, H);
+    int tot;
+    const int ex = block_scan_bool(a, s_cnt, tot);
+    if (a) s_list[n + ex] = j;
+    if (j < nb) s_act[j] = a ? 1 : 0;
+    n += tot;
+  }
+  __syncthreads();
+  if (blockIdx.x == 0) {
+    int run = 0;
+    for (int b0 = 0; b0 < nb; b0 += blockDim.x) {
+      const int j = b0 + t;
+      const bool a = j < nb && s_act[j] != 0;
+      int tot;
+      const int ex = block_scan_bool(a, s_cnt, tot);
+      // Active blocks before j: run + ex; inactive ones: j - run - ex.
+      if (j < nb) p.list_out[a ? run + ex : n + (j - run - ex)] = j;
+      run += tot;
+    }
+    if (t == 0) p.count_out[0] = n;
+  }
+  return n;
+}
+
 // Threads per attention workgroup: NSLOT = kAttendThreads / LPR token rows
 // are in flight per load instruction, R per slot per item.
 constexpr int kAttendThreads = OC_ATTEND_THREADS;
@@ -147,7 +207,9 @@ __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendPar
   constexpr int NWAVE = kAttendThreads / kWave;
 
   static_assert(!LG || NQ <= kLogitsMaxQ, "logits carry at most kLogitsMaxQ queries");
-  __shared__ int s_off[kMaxLists + 1];
+  __shared__ int s_off[kMaxLists + 1];  // item offsets, or the active list in keep-flag mode
+  __shared__ uint8_t s_act[kMaxLists];
+  __shared__ int s_cnt[16];
   __shared__ float s_log[LG ? 1 : NSLOT * V];
   __shared__ float s_o[NWAVE * NQ * D];
   __shared__ float s_m[NWAVE * NQ];
@@ -158,8 +220,11 @@ __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendPar
   const int H = p.num_kv_heads;
   // One segment with one list shared by the heads: no prefix is needed.
   const bool one_unit = !p.per_head && p.num_segments == 1;
-  const int total_items = one_unit ? min(max(p.counts[0], 0), p.total_blocks) * p.nchunk * nqg * H
-                                   : build_item_offsets(p, s_off, nqg);
+  const bool from_keep = p.keep != nullptr;  // one_unit holds (checked on the host)
+  int total_items;
+  if (from_keep) total_items = list_from_keep(p, s_off, s_act, s_cnt) * p.nchunk * nqg * H;
+  else if (one_unit) total_items = min(max(p.counts[0], 0), p.total_blocks) * p.nchunk * nqg * H;
+  else total_items = build_item_offsets(p, s_off, nqg);
 
   const int t = threadIdx.x;
   const int cc = t % LPR;
@@ -191,7 +256,8 @@ __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendPar
     const int h = list - seg * p.num_kv_heads;
     const int off = p.cu_blocks ? p.cu_blocks[seg] : 0;
     const int nbs = p.cu_blocks ? p.cu_blocks[seg + 1] - off : p.total_blocks;
-    const int blk = min(max(p.indices[(p.per_head ? (int64_t)h * p.total_blocks : 0) + off + i], 0), nbs - 1);
+    const int blk = from_keep ? s_off[i]
+                              : min(max(p.indices[(p.per_head ? (int64_t)h * p.total_blocks : 0) + off + i], 0), nbs - 1);
     const int64_t page = page_of(p.pages, p.num_pages, (int64_t)off + blk);
     const int64_t tok0 = page * p.block_size + (int64_t)c * p.chunk;
     const int nrows = min(p.chunk, p.block_size - c * p.chunk);

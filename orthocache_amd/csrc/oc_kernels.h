@@ -28,6 +28,24 @@ struct BandParams {
 hipError_t launch_fwht(const FwhtParams& p, hipStream_t s);
 hipError_t launch_band_energy(const BandParams& p, hipStream_t s);
 
+// Two-gate keep flags written by a scoring kernel: the predicate of the
+// mask + compaction step, keep = (tau_max >= tau) & (zeta <= zeta_max) with
+// fp32 compares (NaN -> false), per segment thresholds when given.
+struct GateParams {
+  uint8_t* keep;          // (total_blocks, Hkv) or null: no flags
+  uint8_t* mask_out;      // (total_blocks, Hkv) or null: a second copy (any alignment)
+  const float* tau_arr;   // (num_segments) or null: tau
+  float tau;
+  const float* zmax_arr;  // (num_segments) or null: zeta_max
+  float zeta_max;
+};
+
+__device__ __forceinline__ uint8_t gate_keep(const GateParams& g, int seg, float tau_max, float zeta) {
+  const float tau = g.tau_arr ? g.tau_arr[seg] : g.tau;
+  const float zm = g.zmax_arr ? g.zmax_arr[seg] : g.zeta_max;
+  return ((tau_max >= tau) & (zeta <= zm)) ? 1 : 0;
+}
+
 // ----------------------------------------------------------- oc_score.hip
 
 struct BoundParams {
@@ -54,6 +72,8 @@ struct CachedBoundParams {
   const int* cu_blocks;  // (num_segments + 1) or null
   int num_segments;
   float* tau_max;      // (total_blocks, Hkv)
+  const float* zeta;   // (total_blocks, Hkv) cached zeta, read for gate.keep
+  GateParams gate;
 };
 
 struct EnergyParams {
@@ -141,6 +161,7 @@ struct ScoreParams {
   // (0 for i >= sq*group); nq_pad = logits_nq_pad(sq * group) <= kLogitsMaxQ.
   float* logits;
   float logit_scale;  // log2(e) / sqrt(head_dim)
+  GateParams gate;    // keep flags from tau_max and zeta (needs q)
 };
 
 constexpr int kLogitsMaxQ = 4;  // query rows per kv head with scoring-pass logits
@@ -194,6 +215,13 @@ struct AttendParams {
   // set, the decode kernel reads them instead of the keys (block_size 512,
   // sq*group <= kLogitsMaxQ); k is not read.
   const float* logits;
+  // Keep flags (total_blocks, Hkv) of one segment instead of a compacted
+  // list (or null): every decode workgroup derives the unified active list
+  // itself; workgroup 0 writes the permutation and count to list_out and
+  // count_out, which the combine then reads (counts must equal count_out).
+  const uint8_t* keep;
+  int* list_out;
+  int* count_out;
 };
 
 bool attend_supported(int dt, int head_dim);

@@ -324,12 +324,13 @@ void score_kernel(ScoreParams p) {
   const float e_mid = 0.125f * tot[1];
   const float e_low = 0.125f * tot[2];
   const float e_ac = e_low + e_mid + e_high;
+  const float zeta = e_high / (e_low + 1e-6f);  // spectral_energy.py:138
   if (t == 0) {
     if (p.e_low) p.e_low[tile] = e_low;
     if (p.e_mid) p.e_mid[tile] = e_mid;
     if (p.e_high) p.e_high[tile] = e_high;
     if (p.e_ac) p.e_ac[tile] = e_ac;
-    if (p.zeta) p.zeta[tile] = e_high / (e_low + 1e-6f);  // spectral_energy.py:138
+    if (p.zeta) p.zeta[tile] = zeta;
   }
 
   // Inline query-aware bound: tau_j = q.kbar/sqrt(d) + ||q|| sqrt(E_AC)/sqrt(d),
@@ -384,7 +385,16 @@ void score_kernel(ScoreParams p) {
         }
       }
     }
-    if (t == 0) p.tau_max[tile] = best;
+    if (t == 0) {
+      p.tau_max[tile] = best;
+      // The two-gate mask of this tile (compute_multiband_mask,
+      // spectral_energy.py:199-234), from the same fp32 scores.
+      if (p.gate.keep) {
+        const uint8_t k = gate_keep(p.gate, seg, best, zeta);
+        p.gate.keep[tile] = k;
+        if (p.gate.mask_out) p.gate.mask_out[tile] = k;
+      }
+    }
   }
 }
 
@@ -570,7 +580,14 @@ __global__ __launch_bounds__(256) void cached_bound_kernel(CachedBoundParams p) 
     const float resid = (sqrtf(b) * sqrt_eac) / sqrt_d;
     best = nanmax(align + resid, best);
   }
-  if (lane == 0) p.tau_max[tile] = best;
+  if (lane == 0) {
+    p.tau_max[tile] = best;
+    if (p.gate.keep) {
+      const uint8_t k = gate_keep(p.gate, seg, best, p.zeta[tile]);
+      p.gate.keep[tile] = k;
+      if (p.gate.mask_out) p.gate.mask_out[tile] = k;
+    }
+  }
 }
 
 template <int QDT>
