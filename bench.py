@@ -4,9 +4,11 @@ Workload: Gemma-style global-attention decode,
 batch 1, 32 query heads over 16 kv heads, head_dim 256, 65,536 tokens (128
 blocks of 512), bf16 K/V, 90% of blocks evicted by the tau quantile.  Inputs
 are synthetic (seeded, generated on the GPU) and resident in HBM before the
-timed region.  A step is one layer: the fused scoring kernel, the mask +
-compaction kernel and the attention (+ combine) kernels, launched on one
-stream with no host synchronisation between them.
+timed region.  A step is one layer (oc_decode_layer): the scoring kernel
+(band statistics, bound, two-gate mask and attention logits in one pass over
+the keys), the attention over the retained blocks (which derives the
+compacted list from the mask) and its combine, launched on one stream with no
+host synchronisation between steps.
 
 Prints one JSON line.  ``value`` is microseconds per layer (lower is better).
 ``roofline`` is for the dominant kernel (block scoring) from HIP events on

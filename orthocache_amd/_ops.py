@@ -520,6 +520,21 @@ class DecodeLayer:
         check(self._fn(self._argp, self._ws_ptr, self._ws_bytes, s), "oc_decode_layer")
         return self.out
 
+    def capture(self) -> "torch.cuda.CUDAGraph":
+        """A HIP graph of one run(): ``replay()`` launches the whole layer with
+        one host call (for launch-bound decode loops).  The graph holds only
+        the layer's kernels (no memset or copy nodes) and the bound buffers:
+        update q, the caches and thresholds in place between replays."""
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self.run()  # first launch outside the capture
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.run()
+        return g
+
     def phases(self):
         """Callables (score, compact, attend) launching the layer's phases one
         at a time on the current stream, with the kernels run() uses (for

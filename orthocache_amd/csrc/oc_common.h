@@ -146,10 +146,41 @@ __device__ __forceinline__ float group_sum(float v) {
 
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<kWave>(v); }
 
+// Value of lane (lane ^ B) for B in {1, 2, 4, 8, 16}, without the LDS
+// crossbar: DPP quad_perm [1,0,3,2] / [2,3,0,1], ds_swizzle bit-mask xor 4
+// and 16 (within 32 lanes), DPP row_ror:8 (xor 8 within a 16-lane row).
+// Lane mappings pinned on gfx950 by an in-bounds probe.
+template <int B>
+__device__ __forceinline__ float lane_xor(float v) {
+  const int x = __float_as_int(v);
+  if constexpr (B == 1) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
+  else if constexpr (B == 2) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+  else if constexpr (B == 4) return __int_as_float(__builtin_amdgcn_ds_swizzle(x, 0x101F));
+  else if constexpr (B == 8) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
+  else if constexpr (B == 16) return __int_as_float(__builtin_amdgcn_ds_swizzle(x, 0x401F));
+  else return __shfl_xor(v, B, kWave);
+}
+
+// One pair step of B = 16 or 32 with v_permlane{16,32}_swap: lanes whose bit
+// B is clear get x + x(lane ^ B), the others y(lane ^ B) + y.  That is the
+// halving-butterfly step for (x, y) = (v[i], v[i + H]) with no selects, and
+// the plain exchange-and-add for x = y.
+template <int B>
+__device__ __forceinline__ float swap_add(float x, float y) {
+  static_assert(B == 16 || B == 32, "row swaps pair 16- or 32-lane rows");
+  if constexpr (B == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+
 // Halving butterfly: sums V per-lane values over groups of LPR lanes.  With
 // V >= LPR, lane l ends with the full sums of value indices
 // [l*V/LPR, (l+1)*V/LPR) in v[0..V/LPR); with V < LPR, v[0] of lane l is the
-// sum of index l / (LPR/V).  V - 1 shuffles for V values instead of
+// sum of index l / (LPR/V).  V - 1 exchanges for V values instead of
 // V log2(LPR).  Instantiate as Butterfly<V, V, LPR / 2, LPR>.
 template <int V, int CNT, int B, int LPR>
 struct Butterfly {
@@ -157,16 +188,22 @@ struct Butterfly {
     if constexpr (B >= 1) {
       if constexpr (CNT > 1) {
         constexpr int H = CNT / 2;
-        const bool upper = (lane & B) != 0;
+        if constexpr (B >= 16) {
 #pragma unroll
-        for (int i = 0; i < H; ++i) {
-          const float send = upper ? v[i] : v[i + H];
-          const float keep = upper ? v[i + H] : v[i];
-          v[i] = keep + __shfl_xor(send, B, LPR);
+          for (int i = 0; i < H; ++i) v[i] = swap_add<B>(v[i], v[i + H]);
+        } else {
+          const bool upper = (lane & B) != 0;
+#pragma unroll
+          for (int i = 0; i < H; ++i) {
+            const float send = upper ? v[i] : v[i + H];
+            const float keep = upper ? v[i + H] : v[i];
+            v[i] = keep + lane_xor<B>(send);
+          }
         }
         Butterfly<V, H, B / 2, LPR>::run(v, lane);
       } else {
-        v[0] += __shfl_xor(v[0], B, LPR);
+        if constexpr (B >= 16) v[0] = swap_add<B>(v[0], v[0]);
+        else v[0] += lane_xor<B>(v[0]);
         Butterfly<V, 1, B / 2, LPR>::run(v, lane);
       }
     }

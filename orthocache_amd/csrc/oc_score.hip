@@ -62,9 +62,12 @@ __device__ __forceinline__ int find_segment(const int* s_cu, int num_segments, i
 // (16-bit keys and queries), 32 lanes per row, two query rows.  Measured on
 // the C2 shape (bf16, head_dim 256): 90 us at three workgroups per CU
 // against 97 us at two.
+// The other bf16 logits variants are held to at least two.  (Some fp16
+// logits variants need more than 256 VGPRs as scheduled and would spill under
+// a floor; they keep the compiler's choice.)
 template <int DT, int LPR, int QDT, int NQL>
 constexpr int score_min_waves() {
-  return (DT != kF32 && QDT == DT && NQL == 2 && LPR == 32) ? 3 : 1;
+  return (DT != kF32 && QDT == DT && NQL == 2 && LPR == 32) ? 3 : ((NQL > 0 && DT == kBF16) ? 2 : 1);
 }
 
 template <int DT, int LPR, int QDT, int NQL>
@@ -207,25 +210,23 @@ void score_kernel(ScoreParams p) {
       for (int c = 0; c < VEC; ++c) column(r, first, c, part);
     }
     if constexpr (NQL > 0) {
-      if constexpr (DOT2) {
-#pragma unroll
-        for (int i = 0; i < V; ++i) part[i] *= p.logit_scale;
-      }
-      // Sum each row's partial dots over its LPR lanes, then stage them.
+      // Sum each row's partial dots over its LPR lanes, then stage them
+      // (packed dot products are scaled once, after the sum).
       Butterfly<V, V, LPR / 2, LPR>::run(part, cc);
+      const float sc = DOT2 ? p.logit_scale : 1.f;
       if constexpr (V >= LPR) {
         constexpr int PER_LANE = V / LPR;
 #pragma unroll
         for (int u = 0; u < PER_LANE; ++u) {
           const int idx = cc * PER_LANE + u;
-          s_lg[(64 * (idx / NQL) + l) * NQL + idx % NQL] = part[u];
+          s_lg[(64 * (idx / NQL) + l) * NQL + idx % NQL] = part[u] * sc;
         }
       } else {
         // REP = LPR / V lanes hold each complete sum; all of them store it
         // (same address, same value), which keeps the loop free of branches.
         constexpr int REP = LPR / V;
         const int idx = cc / REP;
-        s_lg[(64 * (idx / NQL) + l) * NQL + idx % NQL] = part[0];
+        s_lg[(64 * (idx / NQL) + l) * NQL + idx % NQL] = part[0] * sc;
       }
     }
   };

@@ -124,3 +124,29 @@ def test_mask_input_limits(dev):
     q2, k2, v2 = make(dev, 4, 64, 4, 2, 64, torch.bfloat16, seed=2)  # 128 rows per kv head: prefill shapes
     with pytest.raises(_native.OrthoCacheError):
         _ops.attend(q2, k2, v2, None, None, mask=torch.ones(4, 2, dtype=torch.bool, device=dev))
+
+
+def test_layer_graph_replays_match_eager(dev):
+    """The captured layer replayed several times, with eager work and host
+    synchronisation in between and a new query each time, equals the eager
+    layer bit for bit on every replay."""
+    from orthocache_amd import _ops, workloads
+
+    nb, hkv, hq, d = 24, 4, 8, 128
+    k = workloads.make_keys(nb, hkv, d, seed=41, device=dev, noise_blocks=3)
+    v = workloads.make_values(nb * 512, hkv, d, seed=42, device=dev)
+    q = workloads.make_queries((1, hq, d), d, seed=43, device=dev)
+    sc = _ops.score(k, q)
+    tau, zmax = workloads.calibrate_unified(sc.tau_max[0], sc.zeta, evict=0.75)
+    layer = _ops.DecodeLayer(q, k, v, tau, zmax)
+    g = layer.capture()
+    for rep in range(4):
+        layer.q.copy_(workloads.make_queries((1, hq, d), d, seed=50 + rep, device=dev))
+        g.replay()
+        torch.cuda.synchronize()
+        got = (layer.out.clone(), layer.indices.clone(), layer.num_active.clone())
+        _ops.score(k, layer.q)  # unrelated eager work between replays
+        layer.run()
+        torch.cuda.synchronize()
+        assert torch.equal(got[0], layer.out), rep
+        assert torch.equal(got[1], layer.indices) and torch.equal(got[2], layer.num_active), rep
