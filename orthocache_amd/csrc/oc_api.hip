@@ -218,8 +218,8 @@ int make_attend_params(const oc_attend_args* a, oc::AttendParams& p) {
   if ((int64_t)nseg * a->num_kv_heads > oc::kMaxLists)
     return fail(OC_ERR_UNSUPPORTED, "segments x kv heads = %lld exceeds %d", (long long)nseg * a->num_kv_heads, oc::kMaxLists);
   if (a->mask) {
-    if (a->cu_blocks && a->num_segments != 1)
-      return fail(OC_ERR_UNSUPPORTED, "mask input: one segment only (use oc_mask_compact lists for several)");
+    if (a->cu_blocks)
+      return fail(OC_ERR_UNSUPPORTED, "mask input: one segment without cu_blocks (use oc_mask_compact lists for several)");
     if (a->per_head || a->uniform) return fail(OC_ERR_UNSUPPORTED, "mask input: unified lists only");
     if (a->total_blocks < 1 || a->total_blocks > oc::kMaxLists)
       return fail(OC_ERR_UNSUPPORTED, "mask input: 1..%d blocks, got %d", oc::kMaxLists, a->total_blocks);

@@ -455,6 +455,193 @@ __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendPar
   }
 }
 
+// Streaming form of the logits variant, for one segment and a unified list
+// (the decode layer's case): workgroup (split, h) takes a contiguous range
+// [u0, u1) of kv head h's chunks (chunk u: list slot u / nchunk, rows
+// (u % nchunk) * chunk ..), prefetches the next chunk's logits and value rows
+// while it computes the current one, and keeps every row slot's online
+// softmax state (m, l, o) across its chunks.  One partial per (head, split):
+// the combine merges `splits` partials per query row instead of one per
+// 64-row item, and the list is derived (or copied to LDS) once per
+// workgroup instead of once per item.  Splits without chunks write an empty
+// partial (m = -inf, l = 0).
+template <int DT, int LPR, int NQ>
+__global__ __launch_bounds__(kAttendThreads) void attend_stream_kernel(AttendParams p) {
+  using E = Elt<DT>;
+  constexpr int VEC = E::VEC;
+  constexpr int D = LPR * VEC;
+  constexpr int NSLOT = kAttendThreads / LPR;
+  constexpr int ESZ = (DT == kF32) ? 4 : 2;
+  constexpr int R = rows_per_slot<NQ>();
+  constexpr int NWAVE = kAttendThreads / kWave;
+  static_assert(NQ <= kLogitsMaxQ, "logits carry at most kLogitsMaxQ queries");
+
+  __shared__ int s_list[kMaxLists];
+  __shared__ uint8_t s_act[kMaxLists];
+  __shared__ int s_cnt[16];
+  __shared__ float s_o[NWAVE * NQ * D];
+  __shared__ float s_m[NWAVE * NQ];
+  __shared__ float s_l[NWAVE * NQ];
+
+  const int H = p.num_kv_heads;
+  const int h = blockIdx.x % H;
+  const int split = blockIdx.x / H;
+  const int t = threadIdx.x;
+  const int cc = t % LPR;
+  const int slot = t / LPR;
+  const int wave = t / kWave;
+  const int nb = p.total_blocks;
+
+  // The list: derived from the keep flags, or the given one copied to LDS
+  // (entries clamped into the segment).
+  int n;
+  if (p.keep) {
+    n = list_from_keep(p, s_list, s_act, s_cnt);
+  } else {
+    n = min(max(p.counts[0], 0), nb);
+    for (int i = t; i < n; i += blockDim.x) s_list[i] = min(max(p.indices[i], 0), nb - 1);
+    __syncthreads();
+  }
+  const int nu = n * p.nchunk;
+  const int per = (nu + p.splits - 1) / p.splits;
+  const int u0 = min(split * per, nu);
+  const int u1 = min(u0 + per, nu);
+
+  const int64_t vrow = p.v_tok_stride * ESZ;
+  const char* vh = reinterpret_cast<const char*>(p.v) + ((int64_t)h * p.v_head_stride + (int64_t)cc * VEC) * ESZ;
+  // Chunk u's logits (NQ floats per row) and value rows for this lane.
+  auto load = [&](int u, float (&sl)[R][NQ], uint4 (&vw)[R]) {
+    const int i = u / p.nchunk, c = u - i * p.nchunk;
+    const int blk = s_list[i];
+    const int64_t page = page_of(p.pages, p.num_pages, blk);
+    const float* lb = p.logits + (((int64_t)blk * H + h) * kBlock + (int64_t)c * p.chunk) * NQ;
+    const char* vb = vh + (page * kBlock + (int64_t)c * p.chunk) * vrow;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float* lp = lb + (slot + NSLOT * r) * NQ;
+      if constexpr (NQ == 4) {
+        const float4 w = *reinterpret_cast<const float4*>(lp);
+        sl[r][0] = w.x; sl[r][1] = w.y; sl[r][2] = w.z; sl[r][3] = w.w;
+      } else if constexpr (NQ == 2) {
+        const float2 w = *reinterpret_cast<const float2*>(lp);
+        sl[r][0] = w.x; sl[r][1] = w.y;
+      } else {
+        sl[r][0] = lp[0];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) vw[r] = ld16_nt(vb + (int64_t)(slot + NSLOT * r) * vrow);
+  };
+
+  float m[NQ], l[NQ], o[NQ][VEC];
+#pragma unroll
+  for (int g = 0; g < NQ; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) o[g][e] = 0.f;
+  }
+  // Online softmax update of this slot's state with one chunk (all R rows
+  // are in the block: the chunk divides the 512-token block).
+  auto consume = [&](const float (&sl)[R][NQ], const uint4 (&vw)[R]) {
+    float mt[NQ];
+#pragma unroll
+    for (int g = 0; g < NQ; ++g) {
+      float mx = m[g];
+#pragma unroll
+      for (int r = 0; r < R; ++r) mx = fmaxf(mx, sl[r][g]);
+      const float sc = (m[g] == -INFINITY) ? 0.f : exp2f(m[g] - mx);
+      l[g] *= sc;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o[g][e] *= sc;
+      mt[g] = mx;
+      m[g] = mx;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float vx[VEC];
+      E::unpack(vw[r], vx);
+#pragma unroll
+      for (int g = 0; g < NQ; ++g) {
+        const float pw = exp2f(sl[r][g] - mt[g]);
+        l[g] += pw;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[g][e] = fmaf(pw, vx[e], o[g][e]);
+      }
+    }
+  };
+
+  // A ring of NB chunk buffers: chunk u + NB - 1 is requested before chunk u
+  // is consumed (one workgroup per CU, so registers are spent on loads in
+  // flight; measured best at NB = 3 against 2 and 4).
+  constexpr int NB = 3;
+  float sl[NB][R][NQ];
+  uint4 vw[NB][R];
+#pragma unroll
+  for (int j = 0; j < NB - 1; ++j)
+    if (u0 + j < u1) load(u0 + j, sl[j], vw[j]);
+  for (int u = u0; u < u1; u += NB) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      if (u + j < u1) {
+        if (u + j + NB - 1 < u1) load(u + j + NB - 1, sl[(j + NB - 1) % NB], vw[(j + NB - 1) % NB]);
+        consume(sl[j], vw[j]);
+      }
+    }
+  }
+
+  // Merge the slots of this wave (lanes LPR apart) with shuffles.
+#pragma unroll
+  for (int b = LPR; b < kWave; b <<= 1) {
+#pragma unroll
+    for (int g = 0; g < NQ; ++g) {
+      const float m2 = __shfl_xor(m[g], b, kWave);
+      const float l2 = __shfl_xor(l[g], b, kWave);
+      const float mm = fmaxf(m[g], m2);
+      const float w1 = (m[g] == -INFINITY) ? 0.f : exp2f(m[g] - mm);
+      const float w2 = (m2 == -INFINITY) ? 0.f : exp2f(m2 - mm);
+      l[g] = l[g] * w1 + l2 * w2;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float o2 = __shfl_xor(o[g][e], b, kWave);
+        o[g][e] = o[g][e] * w1 + o2 * w2;
+      }
+      m[g] = mm;
+    }
+  }
+  if ((t & (kWave - 1)) < LPR) {
+#pragma unroll
+    for (int g = 0; g < NQ; ++g) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) s_o[(wave * NQ + g) * D + cc * VEC + e] = o[g][e];
+      if (cc == 0) { s_m[wave * NQ + g] = m[g]; s_l[wave * NQ + g] = l[g]; }
+    }
+  }
+  __syncthreads();
+
+  // Merge the waves and write the (head, split) partial, item split * H + h
+  // (the combine's item order for a unified list with one query group).
+  const int64_t item = (int64_t)split * H + h;
+  float* po = p.part_o + item * kQG * D;
+  float* pml = p.part_ml + item * kQG * 2;
+  for (int e = t; e < NQ * D; e += blockDim.x) {
+    const int g = e / D, d = e - g * D;
+    float mm = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) mm = fmaxf(mm, s_m[w * NQ + g]);
+    float acc = 0.f, ll = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) {
+      const float ms = s_m[w * NQ + g];
+      const float wt = (ms == -INFINITY) ? 0.f : exp2f(ms - mm);
+      acc = fmaf(s_o[(w * NQ + g) * D + d], wt, acc);
+      ll = fmaf(s_l[w * NQ + g], wt, ll);
+    }
+    po[g * D + d] = acc;
+    if (d == 0) { pml[2 * g] = mm; pml[2 * g + 1] = ll; }
+  }
+}
+
 // Combine: one workgroup per (output row, 64-wide head_dim slice).  Wave w
 // takes the list's items w, w+4, ... in rounds of kCombineBatch items: each
 // lane requests the partial outputs of the round's items for its column and
@@ -484,7 +671,8 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
   const int qi = st * p.group + g;
   const int qg = qi / kQG, ql = qi - qg * kQG;
   const int list = seg * p.num_kv_heads + h;
-  const int n = list_count(p, list) * p.nchunk;
+  // Streaming form: one partial per split; otherwise one per (slot, chunk).
+  const int n = p.splits > 0 ? p.splits : list_count(p, list) * p.nchunk;
   // Item of the list's j-th (slot, chunk) for query group qg, as the
   // attention kernel enumerates them: head-fastest within the segment for
   // unified lists, list by list for per-head lists.
@@ -543,7 +731,8 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
       a = fmaf(s_acc[w2 * 64 + lane], sw, a);
       ll = fmaf(s_ml[2 * w2 + 1], sw, ll);
     }
-    store_elt(p.out_dtype, p.out, orow + dc * 64 + lane, n == 0 ? 0.f : a / ll);
+    // No retained token (an empty list, or only empty splits): zeros.
+    store_elt(p.out_dtype, p.out, orow + dc * 64 + lane, ll == 0.f ? 0.f : a / ll);
   }
 }
 
@@ -618,8 +807,62 @@ int64_t attend_max_items(const AttendParams& p) {
   return (int64_t)p.num_kv_heads * p.total_blocks * p.nchunk * nqg;
 }
 
-hipError_t launch_attend(const AttendParams& p, hipStream_t s) {
-  if (p.prefill) return launch_prefill(p, s);
+template <int DT, int LPR>
+static hipError_t launch_stream_dt(const AttendParams& p, hipStream_t s) {
+  const dim3 grid(p.num_kv_heads * p.splits);
+  switch (attend_nq_bucket(p.sq * p.group)) {
+    case 1: hipLaunchKernelGGL((attend_stream_kernel<DT, LPR, 1>), grid, dim3(kAttendThreads), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((attend_stream_kernel<DT, LPR, 2>), grid, dim3(kAttendThreads), 0, s, p); break;
+    case 4: hipLaunchKernelGGL((attend_stream_kernel<DT, LPR, 4>), grid, dim3(kAttendThreads), 0, s, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <int DT>
+static hipError_t launch_stream(const AttendParams& p, hipStream_t s) {
+  switch (p.head_dim / Elt<DT>::VEC) {
+    case 8: return launch_stream_dt<DT, 8>(p, s);
+    case 16: return launch_stream_dt<DT, 16>(p, s);
+    case 32: return launch_stream_dt<DT, 32>(p, s);
+    case 64: return launch_stream_dt<DT, 64>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// Splits per kv head for the streaming form, or 0 when it does not apply:
+// about one workgroup per CU (C2 at 90%: 256 workgroups of ~6.5 chunks;
+// measured against 128, 512, 1024 and 2048 workgroups: 26.1, 19.7, 21.4 and
+// 23.2 us against 19.1 for attention + combine), at most one split per chunk
+// of the segment (which keeps the partials inside the per-item workspace).
+int attend_stream_splits(const AttendParams& p) {
+  if (!p.logits || p.per_head || p.cu_blocks || p.prefill || p.block_size != kBlock ||
+      p.total_blocks < 1 || p.total_blocks > kMaxLists || p.uniform || p.sq * p.group > kLogitsMaxQ)
+    return 0;
+  int sp = 256 / p.num_kv_heads;
+  sp = sp < 1 ? 1 : (sp > 64 ? 64 : sp);
+  const int64_t chunks = (int64_t)p.total_blocks * p.nchunk;
+  return (int)(sp < chunks ? sp : chunks);
+}
+
+hipError_t launch_attend(const AttendParams& p_in, hipStream_t s) {
+  if (p_in.prefill) return launch_prefill(p_in, s);
+  AttendParams p = p_in;
+  p.splits = attend_stream_splits(p);
+  if (p.splits > 0) {
+    hipError_t e;
+    switch (p.kv_dtype) {
+      case kF32: e = launch_stream<kF32>(p, s); break;
+      case kBF16: e = launch_stream<kBF16>(p, s); break;
+      case kF16: e = launch_stream<kF16>(p, s); break;
+      default: return hipErrorInvalidValue;
+    }
+    if (e != hipSuccess) return e;
+    const int rows = p.sq * p.num_kv_heads * p.group;
+    const int ndc = (p.head_dim + 63) / 64;
+    hipLaunchKernelGGL(combine_kernel, dim3(rows * ndc), dim3(256), 0, s, p);
+    return hipGetLastError();
+  }
   const int64_t max_items = attend_max_items(p);
   if (max_items > 0) {
     const int grid = (int)(max_items < kAttendGrid ? max_items : kAttendGrid);

@@ -1,6 +1,7 @@
-// Device code of the two-gate mask and stream compaction, shared by the
-// standalone compaction kernel (oc_compact.hip) and the scoring kernel's
-// fused epilogue (oc_score.hip).  Semantics are described in oc_compact.hip.
+// Device code of the two-gate mask and stream compaction: the compaction
+// kernel (oc_compact.hip) and the ballot prefix that the decode attention
+// uses to derive a list from keep flags (oc_attend.hip).  Semantics are
+// described in oc_compact.hip.
 #pragma once
 
 #include "oc_kernels.h"

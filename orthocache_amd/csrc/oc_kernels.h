@@ -222,6 +222,10 @@ struct AttendParams {
   const uint8_t* keep;
   int* list_out;
   int* count_out;
+  // Streaming form (logits, unified list, one segment): each kv head's chunks
+  // are split `splits` ways, one partial per (head, split); 0 = one partial
+  // per work item.
+  int splits;
 };
 
 bool attend_supported(int dt, int head_dim);

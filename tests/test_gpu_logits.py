@@ -166,3 +166,30 @@ def test_decode_layer_uses_logits_and_matches(dev):
     torch.cuda.synchronize()
     assert torch.equal(layer.indices, c.indices) and torch.equal(layer.num_active, c.num_active)
     close(np32(out), np32(ref), 1e-5)
+
+
+@pytest.mark.parametrize("nb,hkv,hq,d,keep", [
+    (1, 1, 1, 128, "all"), (2, 16, 32, 256, "all"), (13, 16, 32, 256, "some"), (128, 16, 32, 256, "some"),
+    (7, 8, 32, 128, "none"), (40, 2, 8, 64, "some"), (300, 4, 4, 128, "some")])
+def test_streaming_attention_edges(dev, nb, hkv, hq, d, keep):
+    """The streaming form (one partial per (head, split); used with logits on
+    one segment) against the key-reading attention and the oracle: a single
+    block, fewer chunks than splits, empty and full lists, long lists."""
+    from orthocache_amd import _ops
+
+    q, k, v = make(dev, nb, 1, hq, hkv, d, torch.bfloat16, seed=nb * 7 + hkv)
+    rng = np.random.default_rng(nb)
+    m_np = {"all": np.ones(nb, bool), "none": np.zeros(nb, bool), "some": rng.random(nb) < 0.3}[keep]
+    mask = torch.from_numpy(m_np).to(dev)
+    c = _ops.mask_compact(num_blocks=nb, num_kv_heads=hkv, device=dev, mask_in=mask)
+    sc = _ops.score(k, q, want_logits=True)
+    out_lg = _ops.attend(q, k, v, c.indices, c.num_active, out_dtype=torch.float32, logits=sc.logits)
+    out_k = _ops.attend(q, k, v, c.indices, c.num_active, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    blocks = [int(j) for j in np.nonzero(m_np)[0]]
+    ref = O.attention_active_blocks(np32(q), np32(k), np32(v), blocks)
+    if not blocks:
+        assert np.all(np32(out_lg) == 0) and np.all(np32(out_k) == 0)
+        return
+    close(np32(out_lg), ref, 2e-3)
+    close(np32(out_lg), np32(out_k), 1e-5)
