@@ -455,27 +455,156 @@ __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendPar
   }
 }
 
-// Streaming form of the logits variant, for one segment and a unified list
-// (the decode layer's case): workgroup (split, h) takes a contiguous range
-// [u0, u1) of kv head h's chunks (chunk u: list slot u / nchunk, rows
-// (u % nchunk) * chunk ..), prefetches the next chunk's logits and value rows
-// while it computes the current one, and keeps every row slot's online
-// softmax state (m, l, o) across its chunks.  One partial per (head, split):
-// the combine merges `splits` partials per query row instead of one per
-// 64-row item, and the list is derived (or copied to LDS) once per
-// workgroup instead of once per item.  Splits without chunks write an empty
-// partial (m = -inf, l = 0).
+// Chunk offsets of the lists for the streaming form: list L = seg * Hkv + h
+// (unified lists share their segment's count, per-head lists have their own)
+// has count_L * nchunk chunks; s_off[L] = chunks of lists before L,
+// s_off[nlists] = total.  keep_n >= 0: one segment whose list has keep_n
+// blocks for every head.  Uniform call; returns the total.
+__device__ int build_list_offsets(const AttendParams& p, int* s_off, int keep_n) {
+  __shared__ int s_wave[16];
+  const int nl = p.num_segments * p.num_kv_heads;
+  const int t = threadIdx.x;
+  const int per = (nl + blockDim.x - 1) / blockDim.x;
+  const int lo = min(t * per, nl);
+  const int hi = min(lo + per, nl);
+  auto chunks = [&](int L) { return (keep_n >= 0 ? keep_n : list_count(p, L)) * p.nchunk; };
+  int sum = 0;
+  for (int i = lo; i < hi; ++i) sum += chunks(i);
+  int total;
+  int run = block_exclusive_scan(sum, s_wave, total);
+  for (int i = lo; i < hi; ++i) {
+    s_off[i] = run;
+    run += chunks(i);
+  }
+  if (t == 0) s_off[nl] = total;
+  __syncthreads();
+  return total;
+}
+
+// Pieces shared by the streaming forms of the logits variant: a chunk is 64
+// (or `chunk`) rows of one block and kv head; a lane holds R rows of its slot
+// and VEC columns, and a row slot's online softmax state (m, l, o) for NQ
+// query rows.
 template <int DT, int LPR, int NQ>
-__global__ __launch_bounds__(kAttendThreads) void attend_stream_kernel(AttendParams p) {
+struct Stream {
   using E = Elt<DT>;
-  constexpr int VEC = E::VEC;
-  constexpr int D = LPR * VEC;
-  constexpr int NSLOT = kAttendThreads / LPR;
-  constexpr int ESZ = (DT == kF32) ? 4 : 2;
-  constexpr int R = rows_per_slot<NQ>();
-  constexpr int NWAVE = kAttendThreads / kWave;
+  static constexpr int VEC = E::VEC;
+  static constexpr int D = LPR * VEC;
+  static constexpr int NSLOT = kAttendThreads / LPR;
+  static constexpr int ESZ = (DT == kF32) ? 4 : 2;
+  static constexpr int R = rows_per_slot<NQ>();
+  static constexpr int NWAVE = kAttendThreads / kWave;
+  // Chunk buffers in flight: chunk g + NB - 1 is requested before chunk g is
+  // consumed (about one workgroup per CU, so registers go to loads in flight;
+  // NB = 3 measured best against 2 and 4).
+  static constexpr int NB = 3;
   static_assert(NQ <= kLogitsMaxQ, "logits carry at most kLogitsMaxQ queries");
 
+  struct State {
+    float m[NQ], l[NQ], o[NQ][VEC];
+  };
+
+  __device__ __forceinline__ static void reset(State& st) {
+#pragma unroll
+    for (int g = 0; g < NQ; ++g) {
+      st.m[g] = -INFINITY;
+      st.l[g] = 0.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) st.o[g][e] = 0.f;
+    }
+  }
+
+  // Logits (NQ floats per row) and value rows of chunk c of flattened block
+  // `flat` (physical page `page`), kv head h.
+  __device__ __forceinline__ static void load(const AttendParams& p, int64_t flat, int64_t page, int h, int c,
+                                              int slot, int cc, float (&sl)[R][NQ], uint4 (&vw)[R]) {
+    const float* lb = p.logits + ((flat * p.num_kv_heads + h) * kBlock + (int64_t)c * p.chunk) * NQ;
+    const int64_t vrow = p.v_tok_stride * ESZ;
+    const char* vb = reinterpret_cast<const char*>(p.v) +
+                     ((page * kBlock + (int64_t)c * p.chunk) * p.v_tok_stride + (int64_t)h * p.v_head_stride +
+                      (int64_t)cc * VEC) * ESZ;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float* lp = lb + (slot + NSLOT * r) * NQ;
+      if constexpr (NQ == 4) {
+        const float4 x = *reinterpret_cast<const float4*>(lp);
+        sl[r][0] = x.x; sl[r][1] = x.y; sl[r][2] = x.z; sl[r][3] = x.w;
+      } else if constexpr (NQ == 2) {
+        const float2 x = *reinterpret_cast<const float2*>(lp);
+        sl[r][0] = x.x; sl[r][1] = x.y;
+      } else {
+        sl[r][0] = lp[0];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) vw[r] = ld16_nt(vb + (int64_t)(slot + NSLOT * r) * vrow);
+  }
+
+  // Online softmax update with one chunk (all R rows are in the block: the
+  // chunk divides the 512-token block).  Uniform lists take equal logits.
+  __device__ __forceinline__ static void consume(State& st, const float (&sl)[R][NQ], const uint4 (&vw)[R],
+                                                 bool uni) {
+    float mt[NQ];
+#pragma unroll
+    for (int g = 0; g < NQ; ++g) {
+      float mx = st.m[g];
+#pragma unroll
+      for (int r = 0; r < R; ++r) mx = fmaxf(mx, uni ? 0.f : sl[r][g]);
+      const float sc = (st.m[g] == -INFINITY) ? 0.f : exp2f(st.m[g] - mx);
+      st.l[g] *= sc;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) st.o[g][e] *= sc;
+      mt[g] = mx;
+      st.m[g] = mx;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float vx[VEC];
+      E::unpack(vw[r], vx);
+#pragma unroll
+      for (int g = 0; g < NQ; ++g) {
+        const float pw = exp2f((uni ? 0.f : sl[r][g]) - mt[g]);
+        st.l[g] += pw;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) st.o[g][e] = fmaf(pw, vx[e], st.o[g][e]);
+      }
+    }
+  }
+
+  // Merge the slots of a wave (lanes LPR apart) with shuffles: lanes
+  // 0..LPR-1 end with the wave's state for their columns.
+  __device__ __forceinline__ static void merge_wave(State& st) {
+#pragma unroll
+    for (int b = LPR; b < kWave; b <<= 1) {
+#pragma unroll
+      for (int g = 0; g < NQ; ++g) {
+        const float m2 = __shfl_xor(st.m[g], b, kWave);
+        const float l2 = __shfl_xor(st.l[g], b, kWave);
+        const float mm = fmaxf(st.m[g], m2);
+        const float w1 = (st.m[g] == -INFINITY) ? 0.f : exp2f(st.m[g] - mm);
+        const float w2 = (m2 == -INFINITY) ? 0.f : exp2f(m2 - mm);
+        st.l[g] = st.l[g] * w1 + l2 * w2;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float o2 = __shfl_xor(st.o[g][e], b, kWave);
+          st.o[g][e] = st.o[g][e] * w1 + o2 * w2;
+        }
+        st.m[g] = mm;
+      }
+    }
+  }
+};
+
+// Split form (kStreamSplit): one segment, a unified list (the one-segment
+// decode layer).  Workgroup (split, h) takes a contiguous range of kv head
+// h's chunks, so concurrently running workgroups read the other heads'
+// pieces of the same token rows; the list is derived from the keep flags or
+// copied to LDS once per workgroup.  At the end the slots merge across waves
+// through LDS into one partial per (head, split), item split * Hkv + h.
+template <int DT, int LPR, int NQ>
+__global__ __launch_bounds__(kAttendThreads) void attend_split_kernel(AttendParams p) {
+  using S = Stream<DT, LPR, NQ>;
+  constexpr int R = S::R, NB = S::NB, D = S::D, VEC = S::VEC, NWAVE = S::NWAVE;
   __shared__ int s_list[kMaxLists];
   __shared__ uint8_t s_act[kMaxLists];
   __shared__ int s_cnt[16];
@@ -492,8 +621,6 @@ __global__ __launch_bounds__(kAttendThreads) void attend_stream_kernel(AttendPar
   const int wave = t / kWave;
   const int nb = p.total_blocks;
 
-  // The list: derived from the keep flags, or the given one copied to LDS
-  // (entries clamped into the segment).
   int n;
   if (p.keep) {
     n = list_from_keep(p, s_list, s_act, s_cnt);
@@ -502,79 +629,25 @@ __global__ __launch_bounds__(kAttendThreads) void attend_stream_kernel(AttendPar
     for (int i = t; i < n; i += blockDim.x) s_list[i] = min(max(p.indices[i], 0), nb - 1);
     __syncthreads();
   }
+  n = __builtin_amdgcn_readfirstlane(n);
   const int nu = n * p.nchunk;
   const int per = (nu + p.splits - 1) / p.splits;
   const int u0 = min(split * per, nu);
   const int u1 = min(u0 + per, nu);
 
-  const int64_t vrow = p.v_tok_stride * ESZ;
-  const char* vh = reinterpret_cast<const char*>(p.v) + ((int64_t)h * p.v_head_stride + (int64_t)cc * VEC) * ESZ;
-  // Chunk u's logits (NQ floats per row) and value rows for this lane.
   auto load = [&](int u, float (&sl)[R][NQ], uint4 (&vw)[R]) {
     const int i = u / p.nchunk, c = u - i * p.nchunk;
-    const int blk = s_list[i];
-    const int64_t page = page_of(p.pages, p.num_pages, blk);
-    const float* lb = p.logits + (((int64_t)blk * H + h) * kBlock + (int64_t)c * p.chunk) * NQ;
-    const char* vb = vh + (page * kBlock + (int64_t)c * p.chunk) * vrow;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float* lp = lb + (slot + NSLOT * r) * NQ;
-      if constexpr (NQ == 4) {
-        const float4 w = *reinterpret_cast<const float4*>(lp);
-        sl[r][0] = w.x; sl[r][1] = w.y; sl[r][2] = w.z; sl[r][3] = w.w;
-      } else if constexpr (NQ == 2) {
-        const float2 w = *reinterpret_cast<const float2*>(lp);
-        sl[r][0] = w.x; sl[r][1] = w.y;
-      } else {
-        sl[r][0] = lp[0];
-      }
+    const int blk = __builtin_amdgcn_readfirstlane(s_list[i]);
+    int64_t page = blk;
+    if (p.pages) {
+      const int pg = ld_const(p.pages + blk);
+      page = (unsigned)pg < (unsigned)p.num_pages ? pg : (pg < 0 ? 0 : p.num_pages - 1);
     }
-#pragma unroll
-    for (int r = 0; r < R; ++r) vw[r] = ld16_nt(vb + (int64_t)(slot + NSLOT * r) * vrow);
+    S::load(p, blk, page, h, c, slot, cc, sl, vw);
   };
 
-  float m[NQ], l[NQ], o[NQ][VEC];
-#pragma unroll
-  for (int g = 0; g < NQ; ++g) {
-    m[g] = -INFINITY;
-    l[g] = 0.f;
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) o[g][e] = 0.f;
-  }
-  // Online softmax update of this slot's state with one chunk (all R rows
-  // are in the block: the chunk divides the 512-token block).
-  auto consume = [&](const float (&sl)[R][NQ], const uint4 (&vw)[R]) {
-    float mt[NQ];
-#pragma unroll
-    for (int g = 0; g < NQ; ++g) {
-      float mx = m[g];
-#pragma unroll
-      for (int r = 0; r < R; ++r) mx = fmaxf(mx, sl[r][g]);
-      const float sc = (m[g] == -INFINITY) ? 0.f : exp2f(m[g] - mx);
-      l[g] *= sc;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) o[g][e] *= sc;
-      mt[g] = mx;
-      m[g] = mx;
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float vx[VEC];
-      E::unpack(vw[r], vx);
-#pragma unroll
-      for (int g = 0; g < NQ; ++g) {
-        const float pw = exp2f(sl[r][g] - mt[g]);
-        l[g] += pw;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) o[g][e] = fmaf(pw, vx[e], o[g][e]);
-      }
-    }
-  };
-
-  // A ring of NB chunk buffers: chunk u + NB - 1 is requested before chunk u
-  // is consumed (one workgroup per CU, so registers are spent on loads in
-  // flight; measured best at NB = 3 against 2 and 4).
-  constexpr int NB = 3;
+  typename S::State st;
+  S::reset(st);
   float sl[NB][R][NQ];
   uint4 vw[NB][R];
 #pragma unroll
@@ -585,42 +658,21 @@ __global__ __launch_bounds__(kAttendThreads) void attend_stream_kernel(AttendPar
     for (int j = 0; j < NB; ++j) {
       if (u + j < u1) {
         if (u + j + NB - 1 < u1) load(u + j + NB - 1, sl[(j + NB - 1) % NB], vw[(j + NB - 1) % NB]);
-        consume(sl[j], vw[j]);
+        S::consume(st, sl[j], vw[j], false);
       }
     }
   }
 
-  // Merge the slots of this wave (lanes LPR apart) with shuffles.
-#pragma unroll
-  for (int b = LPR; b < kWave; b <<= 1) {
-#pragma unroll
-    for (int g = 0; g < NQ; ++g) {
-      const float m2 = __shfl_xor(m[g], b, kWave);
-      const float l2 = __shfl_xor(l[g], b, kWave);
-      const float mm = fmaxf(m[g], m2);
-      const float w1 = (m[g] == -INFINITY) ? 0.f : exp2f(m[g] - mm);
-      const float w2 = (m2 == -INFINITY) ? 0.f : exp2f(m2 - mm);
-      l[g] = l[g] * w1 + l2 * w2;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const float o2 = __shfl_xor(o[g][e], b, kWave);
-        o[g][e] = o[g][e] * w1 + o2 * w2;
-      }
-      m[g] = mm;
-    }
-  }
+  S::merge_wave(st);
   if ((t & (kWave - 1)) < LPR) {
 #pragma unroll
     for (int g = 0; g < NQ; ++g) {
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) s_o[(wave * NQ + g) * D + cc * VEC + e] = o[g][e];
-      if (cc == 0) { s_m[wave * NQ + g] = m[g]; s_l[wave * NQ + g] = l[g]; }
+      for (int e = 0; e < VEC; ++e) s_o[(wave * NQ + g) * D + cc * VEC + e] = st.o[g][e];
+      if (cc == 0) { s_m[wave * NQ + g] = st.m[g]; s_l[wave * NQ + g] = st.l[g]; }
     }
   }
   __syncthreads();
-
-  // Merge the waves and write the (head, split) partial, item split * H + h
-  // (the combine's item order for a unified list with one query group).
   const int64_t item = (int64_t)split * H + h;
   float* po = p.part_o + item * kQG * D;
   float* pml = p.part_ml + item * kQG * 2;
@@ -642,6 +694,128 @@ __global__ __launch_bounds__(kAttendThreads) void attend_stream_kernel(AttendPar
   }
 }
 
+// Ranges form (kStreamRanges): any lists -- several segments, per-head lists,
+// uniform flags.  The chunks of all lists, in list order (list L = seg * Hkv
+// + h; chunk u of a list: list slot u / nchunk, rows (u % nchunk) * chunk ..),
+// form one index space; workgroup w takes the contiguous range
+// [w P, (w + 1) P) of it, P = ceil(total / grid), so every workgroup streams
+// the same number of chunks whatever the lists' lengths.  It keeps the slot
+// states while the chunks belong to one list; when the list changes (and at
+// the end) each wave merges its slots with shuffles and writes its own
+// partial, slot (w + L) * NWAVE + wave: no barrier and no wait on the chunks
+// in flight inside the loop.  Slots are distinct for distinct (w, L) because
+// ranges are monotone in w; the combine finds a list's pieces from the same
+// offsets.  List entries and offsets are read wave-uniformly (readfirstlane,
+// constant-address loads), so the next chunk's list entry is a scalar load
+// that does not wait for the vector loads in flight.
+template <int DT, int LPR, int NQ>
+__global__ __launch_bounds__(kAttendThreads) void attend_stream_kernel(AttendParams p) {
+  using S = Stream<DT, LPR, NQ>;
+  constexpr int R = S::R, NB = S::NB, D = S::D, VEC = S::VEC, NWAVE = S::NWAVE;
+  __shared__ int s_off[kMaxLists + 1];
+
+  const int H = p.num_kv_heads;
+  const int nl = p.num_segments * H;
+  const int w = blockIdx.x;
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int cc = t % LPR;
+  const int slot = t / LPR;
+  const int wave = t / kWave;
+
+  // Values read back from LDS are the same in every lane: readfirstlane
+  // makes that visible to the compiler, so the chunk loop and the addresses
+  // derived from it stay scalar.
+  const int total = __builtin_amdgcn_readfirstlane(build_list_offsets(p, s_off, -1));
+  const int per = (total + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int g0 = min(w * per, total);
+  const int g1 = min(g0 + per, total);
+  if (g0 >= g1) return;  // uniform per workgroup; after the prologue's barriers
+
+  auto uoff = [&](int L) { return __builtin_amdgcn_readfirstlane(s_off[L]); };
+  auto load = [&](int g, int L, float (&sl)[R][NQ], uint4 (&vw)[R]) {
+    const int seg = L / H, h = L - seg * H;
+    const int u = g - uoff(L);
+    const int i = u / p.nchunk, c = u - i * p.nchunk;
+    const int off = p.cu_blocks ? ld_const(p.cu_blocks + seg) : 0;
+    const int nbs = p.cu_blocks ? ld_const(p.cu_blocks + seg + 1) - off : p.total_blocks;
+    const int blk = min(max(ld_const(p.indices + (p.per_head ? (int64_t)h * p.total_blocks : 0) + off + i), 0), nbs - 1);
+    const int64_t flat = (int64_t)off + blk;
+    int64_t page = flat;
+    if (p.pages) {
+      const int pg = ld_const(p.pages + flat);
+      page = (unsigned)pg < (unsigned)p.num_pages ? pg : (pg < 0 ? 0 : p.num_pages - 1);
+    }
+    S::load(p, flat, page, h, c, slot, cc, sl, vw);
+  };
+
+  typename S::State st;
+  // This wave's partial of list L's piece; lanes 0..LPR-1 hold the merged state.
+  auto flush = [&](int L) {
+    S::merge_wave(st);
+    const int64_t item = ((int64_t)w + L) * NWAVE + wave;
+    if (lane < LPR) {
+      float* po = p.part_o + item * kQG * D + cc * VEC;
+#pragma unroll
+      for (int g = 0; g < NQ; ++g) {
+#pragma unroll
+        for (int e = 0; e < VEC; e += 4)
+          *reinterpret_cast<float4*>(po + g * D + e) =
+              make_float4(st.o[g][e], st.o[g][e + 1], st.o[g][e + 2], st.o[g][e + 3]);
+      }
+      if (lane == 0) {
+        float* pml = p.part_ml + item * kQG * 2;
+#pragma unroll
+        for (int g = 0; g < NQ; ++g) { pml[2 * g] = st.m[g]; pml[2 * g + 1] = st.l[g]; }
+      }
+    }
+  };
+  auto is_uniform = [&](int L) { return p.uniform != nullptr && ld_const(p.uniform + L) != 0; };
+  // List of chunk g, from a pointer that only moves forward.
+  auto advance = [&](int L, int g) {
+    while (uoff(L + 1) <= g) ++L;
+    return L;
+  };
+
+  float sl[NB][R][NQ];
+  uint4 vw[NB][R];
+  const int L0 = advance(__builtin_amdgcn_readfirstlane(find_list(s_off, nl, g0)), g0);
+  int Ll = L0;  // list of the next chunk to load
+  int gl = g0;
+#pragma unroll
+  for (int j = 0; j < NB - 1; ++j) {
+    if (gl < g1) {
+      Ll = advance(Ll, gl);
+      load(gl, Ll, sl[j], vw[j]);
+      ++gl;
+    }
+  }
+  int Lc = L0;  // list being accumulated
+  bool uni = is_uniform(Lc);
+  S::reset(st);
+  for (int g = g0; g < g1; g += NB) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      if (g + j < g1) {
+        if (gl < g1) {
+          Ll = advance(Ll, gl);
+          load(gl, Ll, sl[(j + NB - 1) % NB], vw[(j + NB - 1) % NB]);
+          ++gl;
+        }
+        const int Ln = advance(Lc, g + j);
+        if (Ln != Lc) {
+          flush(Lc);
+          S::reset(st);
+          Lc = Ln;
+          uni = is_uniform(Lc);
+        }
+        S::consume(st, sl[j], vw[j], uni);
+      }
+    }
+  }
+  flush(Lc);
+}
+
 // Combine: one workgroup per (output row, 64-wide head_dim slice).  Wave w
 // takes the list's items w, w+4, ... in rounds of kCombineBatch items: each
 // lane requests the partial outputs of the round's items for its column and
@@ -658,7 +832,10 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
   __shared__ float s_acc[4 * 64];
   const int nq_total = p.sq * p.group;
   const int nqg = (nq_total + kQG - 1) / kQG;
-  if (p.per_head || p.num_segments != 1) build_item_offsets(p, s_off, nqg);
+  const bool ranges = p.stream == kStreamRanges;
+  int total = 0;
+  if (ranges) total = build_list_offsets(p, s_off, -1);
+  else if (p.stream == kStreamNone && (p.per_head || p.num_segments != 1)) build_item_offsets(p, s_off, nqg);
   const int D = p.head_dim;
   const int ndc = (D + 63) / 64;
   int id = blockIdx.x;
@@ -671,17 +848,35 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
   const int qi = st * p.group + g;
   const int qg = qi / kQG, ql = qi - qg * kQG;
   const int list = seg * p.num_kv_heads + h;
-  // Streaming form: one partial per split; otherwise one per (slot, chunk).
-  const int n = p.splits > 0 ? p.splits : list_count(p, list) * p.nchunk;
-  // Item of the list's j-th (slot, chunk) for query group qg, as the
-  // attention kernel enumerates them: head-fastest within the segment for
-  // unified lists, list by list for per-head lists.
   const int H = p.num_kv_heads;
+  // Streaming form: the list's pieces are the workgroups fw..lw whose chunk
+  // ranges meet it (P chunks per workgroup), partial slots fw + L .. lw + L.
+  // Otherwise one partial per (slot, chunk) of the list.
+  constexpr int NWS = kAttendThreads / kWave;  // ranges form: partials per piece (one per wave)
+  int n, fw = 0;
+  if (ranges) {
+    const int per = (total + p.splits - 1) / p.splits;
+    const int c0 = s_off[list], c1 = s_off[list + 1];
+    fw = c1 > c0 ? c0 / per : 0;
+    n = c1 > c0 ? ((c1 - 1) / per - fw + 1) * NWS : 0;
+  } else if (p.stream == kStreamSplit) {
+    n = p.splits;  // one partial per split (empty splits hold m = -inf, l = 0)
+  } else {
+    n = list_count(p, list) * p.nchunk;
+  }
+  // Item of the list's j-th partial, i0 + j * istr in every form: per-item
+  // partials are enumerated head-fastest within the segment for unified
+  // lists and list by list for per-head lists; split partials are
+  // split * Hkv + h; ranges partials ((fw + j / NWS) + L) * NWS + j % NWS,
+  // i.e. (fw + L) * NWS + j.
   const bool one_unit = !p.per_head && p.num_segments == 1;
-  const int base = one_unit ? 0 : s_off[p.per_head ? list : seg];
-  auto item_of = [&](int j) -> int64_t {
-    return p.per_head ? (int64_t)(base + j * nqg + qg) : (int64_t)base + (int64_t)(j * nqg + qg) * H + h;
-  };
+  const int base = (one_unit || p.stream != kStreamNone) ? 0 : s_off[p.per_head ? list : seg];
+  int64_t i0, istr;
+  if (ranges) { i0 = ((int64_t)fw + list) * NWS; istr = 1; }
+  else if (p.stream == kStreamSplit) { i0 = h; istr = H; }
+  else if (p.per_head) { i0 = base + qg; istr = nqg; }
+  else { i0 = (int64_t)base + (int64_t)qg * H + h; istr = (int64_t)nqg * H; }
+  auto item_of = [&](int j) -> int64_t { return i0 + (int64_t)j * istr; };
   const int t = threadIdx.x;
   const int lane = t & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
@@ -807,13 +1002,22 @@ int64_t attend_max_items(const AttendParams& p) {
   return (int64_t)p.num_kv_heads * p.total_blocks * p.nchunk * nqg;
 }
 
+template <int DT, int LPR, int NQ>
+static void launch_stream_nq(const AttendParams& p, hipStream_t s) {
+  if (p.stream == kStreamSplit) {
+    hipLaunchKernelGGL((attend_split_kernel<DT, LPR, NQ>), dim3(p.num_kv_heads * p.splits), dim3(kAttendThreads), 0,
+                       s, p);
+  } else {
+    hipLaunchKernelGGL((attend_stream_kernel<DT, LPR, NQ>), dim3(p.splits), dim3(kAttendThreads), 0, s, p);
+  }
+}
+
 template <int DT, int LPR>
 static hipError_t launch_stream_dt(const AttendParams& p, hipStream_t s) {
-  const dim3 grid(p.num_kv_heads * p.splits);
   switch (attend_nq_bucket(p.sq * p.group)) {
-    case 1: hipLaunchKernelGGL((attend_stream_kernel<DT, LPR, 1>), grid, dim3(kAttendThreads), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((attend_stream_kernel<DT, LPR, 2>), grid, dim3(kAttendThreads), 0, s, p); break;
-    case 4: hipLaunchKernelGGL((attend_stream_kernel<DT, LPR, 4>), grid, dim3(kAttendThreads), 0, s, p); break;
+    case 1: launch_stream_nq<DT, LPR, 1>(p, s); break;
+    case 2: launch_stream_nq<DT, LPR, 2>(p, s); break;
+    case 4: launch_stream_nq<DT, LPR, 4>(p, s); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -830,26 +1034,41 @@ static hipError_t launch_stream(const AttendParams& p, hipStream_t s) {
   }
 }
 
-// Splits per kv head for the streaming form, or 0 when it does not apply:
-// about one workgroup per CU (C2 at 90%: 256 workgroups of ~6.5 chunks;
-// measured against 128, 512, 1024 and 2048 workgroups: 26.1, 19.7, 21.4 and
-// 23.2 us against 19.1 for attention + combine), at most one split per chunk
-// of the segment (which keeps the partials inside the per-item workspace).
-int attend_stream_splits(const AttendParams& p) {
-  if (!p.logits || p.per_head || p.cu_blocks || p.prefill || p.block_size != kBlock ||
-      p.total_blocks < 1 || p.total_blocks > kMaxLists || p.uniform || p.sq * p.group > kLogitsMaxQ)
-    return 0;
-  int sp = 256 / p.num_kv_heads;
-  sp = sp < 1 ? 1 : (sp > 64 ? 64 : sp);
+// Which streaming form applies (with logits) and its `splits`: about one
+// workgroup per CU.  C2 at 90%, split form, attention + combine: 128, 256,
+// 512, 1024 and 2048 workgroups gave 26.1, 19.1, 19.7, 21.4 and 23.2 us (a
+// two-chunk ring).  The split form needs one segment and a unified list (its
+// list fits LDS); the ranges form takes any lists, with few enough
+// workgroups that its (w + L) * waves partial slots fit the per-item
+// workspace.
+void attend_stream_plan(AttendParams& p) {
+  p.stream = kStreamNone;
+  p.splits = 0;
+  const int64_t nl = (int64_t)p.num_segments * p.num_kv_heads;
+  if (!p.logits || p.prefill || p.block_size != kBlock || p.total_blocks < 1 || nl > kMaxLists ||
+      p.sq * p.group > kLogitsMaxQ || (p.keep && p.total_blocks > kMaxLists))
+    return;
   const int64_t chunks = (int64_t)p.total_blocks * p.nchunk;
-  return (int)(sp < chunks ? sp : chunks);
+  if (!p.cu_blocks && !p.per_head && !p.uniform && p.total_blocks <= kMaxLists) {
+    int64_t sp = 256 / p.num_kv_heads;
+    sp = sp < 1 ? 1 : (sp > 64 ? 64 : sp);
+    p.stream = kStreamSplit;
+    p.splits = (int)(sp < chunks ? sp : chunks);
+    return;
+  }
+  const int64_t room = attend_max_items(p) / (kAttendThreads / kWave) - nl;
+  const int64_t g = room < 256 ? room : 256;
+  if (g >= 1 && !p.keep) {
+    p.stream = kStreamRanges;
+    p.splits = (int)g;
+  }
 }
 
 hipError_t launch_attend(const AttendParams& p_in, hipStream_t s) {
   if (p_in.prefill) return launch_prefill(p_in, s);
   AttendParams p = p_in;
-  p.splits = attend_stream_splits(p);
-  if (p.splits > 0) {
+  attend_stream_plan(p);
+  if (p.stream != kStreamNone) {
     hipError_t e;
     switch (p.kv_dtype) {
       case kF32: e = launch_stream<kF32>(p, s); break;
@@ -858,7 +1077,7 @@ hipError_t launch_attend(const AttendParams& p_in, hipStream_t s) {
       default: return hipErrorInvalidValue;
     }
     if (e != hipSuccess) return e;
-    const int rows = p.sq * p.num_kv_heads * p.group;
+    const int rows = p.num_segments * p.sq * p.num_kv_heads * p.group;
     const int ndc = (p.head_dim + 63) / 64;
     hipLaunchKernelGGL(combine_kernel, dim3(rows * ndc), dim3(256), 0, s, p);
     return hipGetLastError();

@@ -119,6 +119,16 @@ __device__ __forceinline__ float dot2_acc(uint32_t a, uint32_t b, float acc) {
   }
 }
 
+// Load of data that no lane writes while the kernel runs (lists, counts,
+// segment tables), through the constant address space: with a wave-uniform
+// address this is a scalar load, which waits on its own counter instead of
+// behind the vector loads in flight.
+template <typename T>
+__device__ __forceinline__ T ld_const(const T* p) {
+  typedef const __attribute__((address_space(4))) T ConstT;
+  return *(ConstT*)(p);
+}
+
 // 16-byte global load (the caller guarantees 16-byte alignment).
 __device__ __forceinline__ uint4 ld16(const void* p) {
   return *reinterpret_cast<const uint4*>(p);

@@ -182,6 +182,7 @@ __device__ __forceinline__ int64_t page_of(const int* pages, int num_pages, int6
 
 // ---------------------------------------------------------- oc_attend.hip
 constexpr int kQG = 8;           // queries per attention work item
+enum StreamForm : int { kStreamNone = 0, kStreamSplit = 1, kStreamRanges = 2 };
 constexpr int kMaxLists = 2048;  // (segments x kv heads) per launch
 
 struct AttendParams {
@@ -222,9 +223,12 @@ struct AttendParams {
   const uint8_t* keep;
   int* list_out;
   int* count_out;
-  // Streaming form (logits, unified list, one segment): each kv head's chunks
-  // are split `splits` ways, one partial per (head, split); 0 = one partial
-  // per work item.
+  // Streaming forms (with logits): kStreamSplit (one segment, unified list):
+  // each kv head's chunks split `splits` ways, one partial per (head, split);
+  // kStreamRanges: the chunks of all lists cut into `splits` equal ranges,
+  // one partial per (range, list piece, wave).  kStreamNone: one partial per
+  // work item.
+  int stream;
   int splits;
 };
 

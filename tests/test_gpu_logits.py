@@ -193,3 +193,71 @@ def test_streaming_attention_edges(dev, nb, hkv, hq, d, keep):
         return
     close(np32(out_lg), ref, 2e-3)
     close(np32(out_lg), np32(out_k), 1e-5)
+
+
+@pytest.mark.parametrize("empty_head_all", [False, True])
+def test_streaming_per_head_lists_and_uniform(dev, empty_head_all):
+    """Per-head lists through the logits path, including a head that keeps
+    nothing: zeros (gated kernel) or equal weights over every block (the
+    predicated reference's all-masked softmax, uniform flag)."""
+    from orthocache_amd import _ops
+
+    nb, hkv, hq, d = 6, 3, 6, 128
+    q, k, v = make(dev, nb, 1, hq, hkv, d, torch.bfloat16, seed=19)
+    sc = _ops.score(k, q, want_logits=True)
+    m = np.zeros((nb, hkv), bool)
+    m[[0, 3, 4], 0] = True
+    m[[5], 1] = True  # head 2 keeps nothing
+    mask = torch.from_numpy(m).to(dev)
+    c = _ops.mask_compact(num_blocks=nb, num_kv_heads=hkv, device=dev, mask_in=mask, want_indices=False,
+                          want_head_lists=True, empty_head_all=empty_head_all)
+    kw = dict(per_head=True, uniform=c.head_uniform if empty_head_all else None, out_dtype=torch.float32)
+    out_lg = _ops.attend(q, k, v, c.head_indices, c.head_num_active, logits=sc.logits, **kw)
+    out_k = _ops.attend(q, k, v, c.head_indices, c.head_num_active, **kw)
+    torch.cuda.synchronize()
+    if empty_head_all:
+        ref = O.attention_per_head_predicated(np32(q), np32(k), np32(v), m)
+    else:
+        ref = O.attention_per_head_gated(np32(q), np32(k), np32(v), m)
+    close(np32(out_lg), ref, 2e-3)
+    close(np32(out_lg), np32(out_k), 1e-5)
+
+
+def test_streaming_ragged_segments(dev):
+    """Several segments of very different retained lengths (one empty) through
+    the logits path, against the key-reading attention and the oracle."""
+    from orthocache_amd import _ops
+
+    hkv, hq, d = 4, 16, 128
+    seg_blocks = [9, 1, 30, 4]
+    keep = [[0, 3, 8], [], list(range(0, 30, 2)), [1, 2, 3]]
+    nb = sum(seg_blocks)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(23)
+    k = torch.randn(nb * 512, hkv, d, generator=gen, device=dev).to(torch.bfloat16)
+    v = torch.randn(nb * 512, hkv, d, generator=gen, device=dev).to(torch.bfloat16)
+    q = torch.randn(len(seg_blocks), 1, hq, d, generator=gen, device=dev).to(torch.bfloat16)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(seg_blocks)]), dtype=torch.int32, device=dev)
+    m = np.zeros(nb, bool)
+    off = 0
+    for n, kb in zip(seg_blocks, keep):
+        m[[off + j for j in kb]] = True
+        off += n
+    c = _ops.mask_compact(num_blocks=nb, num_kv_heads=hkv, device=dev, mask_in=torch.from_numpy(m).to(dev),
+                          cu_blocks=cu, num_segments=len(seg_blocks))
+    sc = _ops.score(k, q, cu_blocks=cu, num_segments=len(seg_blocks), want_logits=True)
+    kw = dict(cu_blocks=cu, num_segments=len(seg_blocks), out_dtype=torch.float32)
+    out_lg = _ops.attend(q, k, v, c.indices, c.num_active, logits=sc.logits, **kw)
+    out_k = _ops.attend(q, k, v, c.indices, c.num_active, **kw)
+    torch.cuda.synchronize()
+    close(np32(out_lg), np32(out_k), 1e-5)
+    off = 0
+    qn, kn, vn = np32(q), np32(k), np32(v)
+    for s, (n, kb) in enumerate(zip(seg_blocks, keep)):
+        ks, vs = kn[off * 512:(off + n) * 512], vn[off * 512:(off + n) * 512]
+        ref = O.attention_active_blocks(qn[s], ks, vs, kb)
+        if kb:
+            close(np32(out_lg)[s], ref, 2e-3)
+        else:
+            assert np.all(np32(out_lg)[s] == 0)
+        off += n
