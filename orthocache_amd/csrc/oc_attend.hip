@@ -481,13 +481,18 @@ __device__ int build_list_offsets(const AttendParams& p, int* s_off, int keep_n)
   return total;
 }
 
-// Pieces shared by the streaming forms of the logits variant: a chunk is 64
-// (or `chunk`) rows of one block and kv head; a lane holds R rows of its slot
-// and VEC columns, and a row slot's online softmax state (m, l, o) for NQ
-// query rows.
-template <int DT, int LPR, int NQ>
+// Pieces shared by the streaming forms: a chunk is `chunk` rows of one block
+// and kv head; a lane holds R rows of its slot and VEC columns, and a row
+// slot's online softmax state (m, l, o) for NQ query rows.  KV = false: the
+// chunk's logits come from the scoring pass (values and logits are read);
+// KV = true: keys and values are read and the logits formed here (the lane's
+// partial dot products summed over the row's LPR lanes with the halving
+// butterfly, then gathered to every lane of the slot with shuffles, so no
+// LDS barrier interrupts the loads in flight).
+template <int DT, int LPR, int NQ, bool KV = false, int QDT = DT>
 struct Stream {
   using E = Elt<DT>;
+  using EQ = Elt<QDT>;
   static constexpr int VEC = E::VEC;
   static constexpr int D = LPR * VEC;
   static constexpr int NSLOT = kAttendThreads / LPR;
@@ -496,12 +501,23 @@ struct Stream {
   static constexpr int NWAVE = kAttendThreads / kWave;
   // Chunk buffers in flight: chunk g + NB - 1 is requested before chunk g is
   // consumed (about one workgroup per CU, so registers go to loads in flight;
-  // NB = 3 measured best against 2 and 4).
-  static constexpr int NB = 3;
-  static_assert(NQ <= kLogitsMaxQ, "logits carry at most kLogitsMaxQ queries");
+  // with logits NB = 3 measured best against 2 and 4; keys and values take
+  // twice the registers per chunk).
+  static constexpr int NB = KV ? 2 : 3;
+  static_assert(NQ <= kLogitsMaxQ, "the streaming forms carry at most kLogitsMaxQ queries");
 
   struct State {
     float m[NQ], l[NQ], o[NQ][VEC];
+  };
+  // One chunk in flight: value rows, and logits (KV = false) or key rows.
+  struct Buf {
+    uint4 vw[R];
+    float sl[KV ? 1 : R][NQ];
+    uint4 kw[KV ? R : 1];
+  };
+  // The lane's query columns, pre-scaled by log2(e)/sqrt(d) (KV = true).
+  struct Query {
+    float q[KV ? NQ : 1][VEC];
   };
 
   __device__ __forceinline__ static void reset(State& st) {
@@ -514,36 +530,112 @@ struct Stream {
     }
   }
 
-  // Logits (NQ floats per row) and value rows of chunk c of flattened block
-  // `flat` (physical page `page`), kv head h.
+  // Chunk c of flattened block `flat` (physical page `page`), kv head h:
+  // logits (NQ floats per row) or key rows, then value rows.
   __device__ __forceinline__ static void load(const AttendParams& p, int64_t flat, int64_t page, int h, int c,
-                                              int slot, int cc, float (&sl)[R][NQ], uint4 (&vw)[R]) {
-    const float* lb = p.logits + ((flat * p.num_kv_heads + h) * kBlock + (int64_t)c * p.chunk) * NQ;
-    const int64_t vrow = p.v_tok_stride * ESZ;
-    const char* vb = reinterpret_cast<const char*>(p.v) +
-                     ((page * kBlock + (int64_t)c * p.chunk) * p.v_tok_stride + (int64_t)h * p.v_head_stride +
-                      (int64_t)cc * VEC) * ESZ;
+                                              int slot, int cc, Buf& b) {
+    const int64_t tok0 = page * kBlock + (int64_t)c * p.chunk;
+    if constexpr (KV) {
+      const int64_t krow = p.k_tok_stride * ESZ;
+      const char* kb = reinterpret_cast<const char*>(p.k) +
+                       (tok0 * p.k_tok_stride + (int64_t)h * p.k_head_stride + (int64_t)cc * VEC) * ESZ;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float* lp = lb + (slot + NSLOT * r) * NQ;
-      if constexpr (NQ == 4) {
-        const float4 x = *reinterpret_cast<const float4*>(lp);
-        sl[r][0] = x.x; sl[r][1] = x.y; sl[r][2] = x.z; sl[r][3] = x.w;
-      } else if constexpr (NQ == 2) {
-        const float2 x = *reinterpret_cast<const float2*>(lp);
-        sl[r][0] = x.x; sl[r][1] = x.y;
-      } else {
-        sl[r][0] = lp[0];
+      for (int r = 0; r < R; ++r) b.kw[r] = ld16_nt(kb + (int64_t)(slot + NSLOT * r) * krow);
+    } else {
+      const float* lb = p.logits + ((flat * p.num_kv_heads + h) * kBlock + (int64_t)c * p.chunk) * NQ;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float* lp = lb + (slot + NSLOT * r) * NQ;
+        if constexpr (NQ == 4) {
+          const float4 x = *reinterpret_cast<const float4*>(lp);
+          b.sl[r][0] = x.x; b.sl[r][1] = x.y; b.sl[r][2] = x.z; b.sl[r][3] = x.w;
+        } else if constexpr (NQ == 2) {
+          const float2 x = *reinterpret_cast<const float2*>(lp);
+          b.sl[r][0] = x.x; b.sl[r][1] = x.y;
+        } else {
+          b.sl[r][0] = lp[0];
+        }
       }
     }
+    const int64_t vrow = p.v_tok_stride * ESZ;
+    const char* vb = reinterpret_cast<const char*>(p.v) +
+                     (tok0 * p.v_tok_stride + (int64_t)h * p.v_head_stride + (int64_t)cc * VEC) * ESZ;
 #pragma unroll
-    for (int r = 0; r < R; ++r) vw[r] = ld16_nt(vb + (int64_t)(slot + NSLOT * r) * vrow);
+    for (int r = 0; r < R; ++r) b.vw[r] = ld16_nt(vb + (int64_t)(slot + NSLOT * r) * vrow);
+  }
+
+  // The query rows of list (seg, h), this lane's VEC columns (KV = true).
+  __device__ __forceinline__ static void load_query(const AttendParams& p, int seg, int h, int cc, Query& qr) {
+    if constexpr (KV) {
+      constexpr int QSZ = (QDT == kF32) ? 4 : 2;
+      const int nq = p.sq * p.group;
+#pragma unroll
+      for (int g = 0; g < NQ; ++g) {
+        const int qc = min(g, nq - 1);
+        const int st = qc / p.group, gg = qc - st * p.group;
+        const char* qp = reinterpret_cast<const char*>(p.q) +
+                         ((int64_t)seg * p.q_seg_stride + (int64_t)st * p.q_tok_stride +
+                          (int64_t)(h * p.group + gg) * p.q_head_stride + (int64_t)cc * VEC) * QSZ;
+        const float sc = g < nq ? p.logit_scale : 0.f;
+#pragma unroll
+        for (int e0 = 0; e0 < VEC; e0 += EQ::VEC) {
+          float tmp[EQ::VEC];
+          EQ::unpack(ld16(qp + e0 * QSZ), tmp);
+#pragma unroll
+          for (int e = 0; e < EQ::VEC && e0 + e < VEC; ++e) qr.q[g][e0 + e] = tmp[e] * sc;
+        }
+      }
+    }
+  }
+
+  // The chunk's logits in the log2 domain, every row of the lane's slot:
+  // given (KV = false) or formed from the keys (KV = true).
+  __device__ __forceinline__ static void logits(const Buf& b, const Query& qr, int cc, float (&lg)[R][NQ]) {
+    if constexpr (!KV) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int g = 0; g < NQ; ++g) lg[r][g] = b.sl[r][g];
+    } else {
+      constexpr int V = R * NQ;  // value index r * NQ + g
+      float part[V];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float kx[VEC];
+        E::unpack(b.kw[r], kx);
+#pragma unroll
+        for (int g = 0; g < NQ; ++g) {
+          float d = 0.f;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) d = fmaf(qr.q[g][e], kx[e], d);
+          part[r * NQ + g] = d;
+        }
+      }
+      Butterfly<V, V, LPR / 2, LPR>::run(part, cc);
+      // Gather the V sums to every lane of the slot (width-LPR shuffles).
+      if constexpr (V >= LPR) {
+        constexpr int PL = V / LPR;  // lane s holds indices s * PL .. + PL
+#pragma unroll
+        for (int u = 0; u < PL; ++u)
+#pragma unroll
+          for (int src = 0; src < LPR; ++src) {
+            const int idx = src * PL + u;
+            lg[idx / NQ][idx % NQ] = __shfl(part[u], src, LPR);
+          }
+      } else {
+        constexpr int REP = LPR / V;  // lanes idx * REP .. hold index idx
+#pragma unroll
+        for (int idx = 0; idx < V; ++idx) lg[idx / NQ][idx % NQ] = __shfl(part[0], idx * REP, LPR);
+      }
+    }
   }
 
   // Online softmax update with one chunk (all R rows are in the block: the
   // chunk divides the 512-token block).  Uniform lists take equal logits.
-  __device__ __forceinline__ static void consume(State& st, const float (&sl)[R][NQ], const uint4 (&vw)[R],
-                                                 bool uni) {
+  __device__ __forceinline__ static void consume(State& st, const Buf& b, const Query& qr, int cc, bool uni) {
+    float sl[R][NQ];
+    logits(b, qr, cc, sl);
+    const uint4 (&vw)[R] = b.vw;
     float mt[NQ];
 #pragma unroll
     for (int g = 0; g < NQ; ++g) {
@@ -601,9 +693,9 @@ struct Stream {
 // pieces of the same token rows; the list is derived from the keep flags or
 // copied to LDS once per workgroup.  At the end the slots merge across waves
 // through LDS into one partial per (head, split), item split * Hkv + h.
-template <int DT, int LPR, int NQ>
+template <int DT, int LPR, int NQ, bool KV, int QDT>
 __global__ __launch_bounds__(kAttendThreads) void attend_split_kernel(AttendParams p) {
-  using S = Stream<DT, LPR, NQ>;
+  using S = Stream<DT, LPR, NQ, KV, QDT>;
   constexpr int R = S::R, NB = S::NB, D = S::D, VEC = S::VEC, NWAVE = S::NWAVE;
   __shared__ int s_list[kMaxLists];
   __shared__ uint8_t s_act[kMaxLists];
@@ -635,7 +727,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_split_kernel(AttendPara
   const int u0 = min(split * per, nu);
   const int u1 = min(u0 + per, nu);
 
-  auto load = [&](int u, float (&sl)[R][NQ], uint4 (&vw)[R]) {
+  auto load = [&](int u, typename S::Buf& b) {
     const int i = u / p.nchunk, c = u - i * p.nchunk;
     const int blk = __builtin_amdgcn_readfirstlane(s_list[i]);
     int64_t page = blk;
@@ -643,22 +735,23 @@ __global__ __launch_bounds__(kAttendThreads) void attend_split_kernel(AttendPara
       const int pg = ld_const(p.pages + blk);
       page = (unsigned)pg < (unsigned)p.num_pages ? pg : (pg < 0 ? 0 : p.num_pages - 1);
     }
-    S::load(p, blk, page, h, c, slot, cc, sl, vw);
+    S::load(p, blk, page, h, c, slot, cc, b);
   };
 
   typename S::State st;
   S::reset(st);
-  float sl[NB][R][NQ];
-  uint4 vw[NB][R];
+  typename S::Query qr;
+  S::load_query(p, 0, h, cc, qr);
+  typename S::Buf buf[NB];
 #pragma unroll
   for (int j = 0; j < NB - 1; ++j)
-    if (u0 + j < u1) load(u0 + j, sl[j], vw[j]);
+    if (u0 + j < u1) load(u0 + j, buf[j]);
   for (int u = u0; u < u1; u += NB) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       if (u + j < u1) {
-        if (u + j + NB - 1 < u1) load(u + j + NB - 1, sl[(j + NB - 1) % NB], vw[(j + NB - 1) % NB]);
-        S::consume(st, sl[j], vw[j], false);
+        if (u + j + NB - 1 < u1) load(u + j + NB - 1, buf[(j + NB - 1) % NB]);
+        S::consume(st, buf[j], qr, cc, false);
       }
     }
   }
@@ -708,9 +801,9 @@ __global__ __launch_bounds__(kAttendThreads) void attend_split_kernel(AttendPara
 // offsets.  List entries and offsets are read wave-uniformly (readfirstlane,
 // constant-address loads), so the next chunk's list entry is a scalar load
 // that does not wait for the vector loads in flight.
-template <int DT, int LPR, int NQ>
+template <int DT, int LPR, int NQ, bool KV, int QDT>
 __global__ __launch_bounds__(kAttendThreads) void attend_stream_kernel(AttendParams p) {
-  using S = Stream<DT, LPR, NQ>;
+  using S = Stream<DT, LPR, NQ, KV, QDT>;
   constexpr int R = S::R, NB = S::NB, D = S::D, VEC = S::VEC, NWAVE = S::NWAVE;
   __shared__ int s_off[kMaxLists + 1];
 
@@ -733,7 +826,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_stream_kernel(AttendPar
   if (g0 >= g1) return;  // uniform per workgroup; after the prologue's barriers
 
   auto uoff = [&](int L) { return __builtin_amdgcn_readfirstlane(s_off[L]); };
-  auto load = [&](int g, int L, float (&sl)[R][NQ], uint4 (&vw)[R]) {
+  auto load = [&](int g, int L, typename S::Buf& b) {
     const int seg = L / H, h = L - seg * H;
     const int u = g - uoff(L);
     const int i = u / p.nchunk, c = u - i * p.nchunk;
@@ -746,10 +839,11 @@ __global__ __launch_bounds__(kAttendThreads) void attend_stream_kernel(AttendPar
       const int pg = ld_const(p.pages + flat);
       page = (unsigned)pg < (unsigned)p.num_pages ? pg : (pg < 0 ? 0 : p.num_pages - 1);
     }
-    S::load(p, flat, page, h, c, slot, cc, sl, vw);
+    S::load(p, flat, page, h, c, slot, cc, b);
   };
 
   typename S::State st;
+  typename S::Query qr;
   // This wave's partial of list L's piece; lanes 0..LPR-1 hold the merged state.
   auto flush = [&](int L) {
     S::merge_wave(st);
@@ -777,20 +871,20 @@ __global__ __launch_bounds__(kAttendThreads) void attend_stream_kernel(AttendPar
     return L;
   };
 
-  float sl[NB][R][NQ];
-  uint4 vw[NB][R];
+  typename S::Buf buf[NB];
   const int L0 = advance(__builtin_amdgcn_readfirstlane(find_list(s_off, nl, g0)), g0);
+  int Lc = L0;  // list being accumulated
+  S::load_query(p, Lc / H, Lc - (Lc / H) * H, cc, qr);
   int Ll = L0;  // list of the next chunk to load
   int gl = g0;
 #pragma unroll
   for (int j = 0; j < NB - 1; ++j) {
     if (gl < g1) {
       Ll = advance(Ll, gl);
-      load(gl, Ll, sl[j], vw[j]);
+      load(gl, Ll, buf[j]);
       ++gl;
     }
   }
-  int Lc = L0;  // list being accumulated
   bool uni = is_uniform(Lc);
   S::reset(st);
   for (int g = g0; g < g1; g += NB) {
@@ -799,7 +893,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_stream_kernel(AttendPar
       if (g + j < g1) {
         if (gl < g1) {
           Ll = advance(Ll, gl);
-          load(gl, Ll, sl[(j + NB - 1) % NB], vw[(j + NB - 1) % NB]);
+          load(gl, Ll, buf[(j + NB - 1) % NB]);
           ++gl;
         }
         const int Ln = advance(Lc, g + j);
@@ -808,8 +902,9 @@ __global__ __launch_bounds__(kAttendThreads) void attend_stream_kernel(AttendPar
           S::reset(st);
           Lc = Ln;
           uni = is_uniform(Lc);
+          S::load_query(p, Lc / H, Lc - (Lc / H) * H, cc, qr);  // keys need the new list's queries
         }
-        S::consume(st, sl[j], vw[j], uni);
+        S::consume(st, buf[j], qr, cc, uni);
       }
     }
   }
@@ -1002,25 +1097,40 @@ int64_t attend_max_items(const AttendParams& p) {
   return (int64_t)p.num_kv_heads * p.total_blocks * p.nchunk * nqg;
 }
 
-template <int DT, int LPR, int NQ>
-static void launch_stream_nq(const AttendParams& p, hipStream_t s) {
+template <int DT, int LPR, int NQ, bool KV, int QDT>
+static void launch_stream_k(const AttendParams& p, hipStream_t s) {
   if (p.stream == kStreamSplit) {
-    hipLaunchKernelGGL((attend_split_kernel<DT, LPR, NQ>), dim3(p.num_kv_heads * p.splits), dim3(kAttendThreads), 0,
-                       s, p);
+    hipLaunchKernelGGL((attend_split_kernel<DT, LPR, NQ, KV, QDT>), dim3(p.num_kv_heads * p.splits),
+                       dim3(kAttendThreads), 0, s, p);
   } else {
-    hipLaunchKernelGGL((attend_stream_kernel<DT, LPR, NQ>), dim3(p.splits), dim3(kAttendThreads), 0, s, p);
+    hipLaunchKernelGGL((attend_stream_kernel<DT, LPR, NQ, KV, QDT>), dim3(p.splits), dim3(kAttendThreads), 0, s, p);
   }
+}
+
+template <int DT, int LPR, int NQ>
+static hipError_t launch_stream_nq(const AttendParams& p, hipStream_t s) {
+  if (p.logits) {
+    launch_stream_k<DT, LPR, NQ, false, DT>(p, s);
+  } else if (p.q_dtype == DT) {
+    launch_stream_k<DT, LPR, NQ, true, DT>(p, s);
+  } else if (p.q_dtype == kF32) {
+    launch_stream_k<DT, LPR, NQ, true, kF32>(p, s);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipSuccess;
 }
 
 template <int DT, int LPR>
 static hipError_t launch_stream_dt(const AttendParams& p, hipStream_t s) {
+  hipError_t e;
   switch (attend_nq_bucket(p.sq * p.group)) {
-    case 1: launch_stream_nq<DT, LPR, 1>(p, s); break;
-    case 2: launch_stream_nq<DT, LPR, 2>(p, s); break;
-    case 4: launch_stream_nq<DT, LPR, 4>(p, s); break;
+    case 1: e = launch_stream_nq<DT, LPR, 1>(p, s); break;
+    case 2: e = launch_stream_nq<DT, LPR, 2>(p, s); break;
+    case 4: e = launch_stream_nq<DT, LPR, 4>(p, s); break;
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
+  return e != hipSuccess ? e : hipGetLastError();
 }
 
 template <int DT>
@@ -1034,19 +1144,20 @@ static hipError_t launch_stream(const AttendParams& p, hipStream_t s) {
   }
 }
 
-// Which streaming form applies (with logits) and its `splits`: about one
-// workgroup per CU.  C2 at 90%, split form, attention + combine: 128, 256,
-// 512, 1024 and 2048 workgroups gave 26.1, 19.1, 19.7, 21.4 and 23.2 us (a
-// two-chunk ring).  The split form needs one segment and a unified list (its
-// list fits LDS); the ranges form takes any lists, with few enough
-// workgroups that its (w + L) * waves partial slots fit the per-item
-// workspace.
+// Which streaming form applies and its `splits`: about one workgroup per CU.
+// C2 at 90%, split form with logits, attention + combine: 128, 256, 512, 1024
+// and 2048 workgroups gave 26.1, 19.1, 19.7, 21.4 and 23.2 us (a two-chunk
+// ring).  At most 4 query rows per kv head and whole 512-token blocks; keys
+// and values (no logits) also need a block of whole chunks.  The split form
+// needs one segment and a unified list (its list fits LDS); the ranges form
+// takes any lists, with few enough workgroups that its (w + L) * waves
+// partial slots fit the per-item workspace.
 void attend_stream_plan(AttendParams& p) {
   p.stream = kStreamNone;
   p.splits = 0;
   const int64_t nl = (int64_t)p.num_segments * p.num_kv_heads;
-  if (!p.logits || p.prefill || p.block_size != kBlock || p.total_blocks < 1 || nl > kMaxLists ||
-      p.sq * p.group > kLogitsMaxQ || (p.keep && p.total_blocks > kMaxLists))
+  if (p.prefill || p.block_size != kBlock || p.total_blocks < 1 || nl > kMaxLists ||
+      p.sq * p.group > kLogitsMaxQ || (p.keep && p.total_blocks > kMaxLists) || kBlock % p.chunk != 0)
     return;
   const int64_t chunks = (int64_t)p.total_blocks * p.nchunk;
   if (!p.cu_blocks && !p.per_head && !p.uniform && p.total_blocks <= kMaxLists) {
