@@ -184,6 +184,18 @@ def main():
     us_per_layer = wall * 1e6 / args.steps
     layer_event_us = event_time_us(layer.run, args.steps, torch)
 
+    # The configuration's eviction sweep (50/75/90% by the tau quantile),
+    # each a separate layer over the same inputs, timed with HIP events.
+    sweep = {}
+    for ev in (0.5, 0.75, 0.9):
+        t_ev, z_ev = workloads.calibrate_unified(sc.tau_max[0], sc.zeta, ev)
+        lay = _ops.DecodeLayer(wl.q, wl.k, wl.v, t_ev, z_ev)
+        for _ in range(args.warmup):
+            lay.run()
+        sweep[str(ev)] = {"us": round(event_time_us(lay.run, args.steps, torch), 2),
+                          "num_active": int(lay.num_active[0].item())}
+        del lay
+
     score_us = event_time_us(score_fn, args.kernel_reps, torch)
     # One segment: no compaction launch (the attention derives the list).
     compact_us = event_time_us(compact_fn, args.kernel_reps, torch) if compact_fn else 0.0
@@ -244,6 +256,7 @@ def main():
         "layer_gbps": round(layer_bytes / (us_per_layer * 1e-6) / 1e9, 1),
         "layer_frac_of_peak": round(layer_bytes / (us_per_layer * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
         "layer_event_us": round(layer_event_us, 2),
+        "evict_sweep": sweep,
         "algorithmic_bytes": {"score": score_bytes, "compact": compact_bytes, "attend": attend_bytes,
                               "layer": moved_bytes, "layer_model": layer_bytes},
         "scoring_pass_logits": logits,
