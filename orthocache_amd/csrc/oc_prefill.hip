@@ -47,6 +47,8 @@ constexpr int kPfRows = kPrefillRows;
 static_assert(kPfRows == kPfWaves * 32, "one 32-row MFMA tile per wave");
 constexpr int kPfKeys = 64;             // keys per tile
 constexpr float kLazy = 8.f;            // log2 headroom before the softmax reference moves
+// (1, 1) as a packed pair of the operand type, for row sums by dot2.
+template <int DT> constexpr uint32_t kOnePair = DT == kBF16 ? 0x3f803f80u : 0x3c003c00u;
 
 template <int DT> struct Mma;
 template <> struct Mma<kBF16> {
@@ -128,8 +130,16 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
   constexpr int NDCH = D / 8;                // 16-byte chunks per row
   static_assert(KCH >= 1 && (KPT == 2 || KPT == 4), "unsupported head_dim");
 
-  __shared__ __align__(16) char s_k[kPfKeys * KROW];
-  __shared__ __align__(16) char s_v[D * kPfKeys * 2];
+  constexpr int KBYTES = kPfKeys * KROW;     // one K tile in LDS
+  constexpr int VBYTES = D * kPfKeys * 2;    // one V^T tile in LDS
+  // Two buffers each (separate objects, so the compiler sees that loads into
+  // one never alias reads of the other): while tile j's softmax and P V run,
+  // tile j+1's K is already in LDS for its Q K^T, and K_{j+2} and V_{j+1} go
+  // to the buffers tile j-1 has released -- one barrier per tile.
+  __shared__ __align__(16) char s_k0[KBYTES];
+  __shared__ __align__(16) char s_k1[KBYTES];
+  __shared__ __align__(16) char s_v0[VBYTES];
+  __shared__ __align__(16) char s_v1[VBYTES];
 
   const int nq_rows = prefill_rows(p);
   const int nqt = (nq_rows + kPfRows - 1) / kPfRows;
@@ -153,7 +163,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
   const int ntiles = count * tpb;
   const int per = (ntiles + p.nsplit - 1) / p.nsplit;
   const int t0 = min(split * per, ntiles);
-  const int t1 = min(t0 + per, ntiles);
+  const int n = min(t0 + per, ntiles) - t0;  // tiles of this split
   const bool uni = (p.uniform != nullptr) && (p.uniform[list] != 0);
   const int* idx = p.indices + (p.per_head ? (int64_t)h * p.total_blocks : 0) + off;
 
@@ -163,7 +173,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
   const int hf = lane >> 5;
   const int q32 = lane & 31;
 
-  // Q^T slices (B operand): row r, 8 dims at 16 ds + 8 hf.
+  // Q^T slices (B operand): row r, 8 dims at 16 ds + 8 hf.  A uniform list
+  // takes equal logits: zero query fragments make every S entry exactly 0.
   const int row = qt * kPfRows + wave * 32 + q32;
   u32x4_t qf[DS];
   {
@@ -173,15 +184,21 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
                      ((int64_t)seg * p.q_seg_stride + (int64_t)st * p.q_tok_stride +
                       (int64_t)(h * p.group + g) * p.q_head_stride + 8 * hf) * 2;
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds) qf[ds] = ld16v(qp + ds * 32);
+    for (int ds = 0; ds < DS; ++ds) {
+      qf[ds] = ld16v(qp + ds * 32);
+      if (uni) qf[ds] = u32x4_t{0u, 0u, 0u, 0u};
+    }
   }
 
   const int64_t krow_g = p.k_tok_stride * 2, vrow_g = p.v_tok_stride * 2;
   const char* kbase = reinterpret_cast<const char*>(p.k) + (int64_t)h * p.k_head_stride * 2;
   const char* vbase = reinterpret_cast<const char*>(p.v) + (int64_t)h * p.v_head_stride * 2;
 
-  // This thread's share of a tile: K chunks c = t + 256 u (key c / NDCH,
-  // chunk c % NDCH); V keys vk0 .. vk0 + KPT - 1 at chunk vdch.
+  // This thread's share of a tile: K chunks c = t + 256 u, loaded straight
+  // into LDS (lane l of a wave writes 16 bytes at the instruction's base +
+  // 16 l), so LDS chunk c -- row c / NDCH, swizzled position c % NDCH -- is
+  // fetched from the global chunk the swizzle puts there; V keys
+  // vk0 .. vk0 + KPT - 1 at chunk vdch, through registers for the transpose.
   // Lane -> (16-byte chunk, key group) of the V transpose.  For head_dim 128
   // the 16 lanes of an LDS write phase cover 8 dims x 2 key groups whose
   // positions differ in the 8-byte half of a block, so the writes spread over
@@ -200,30 +217,43 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
 #pragma unroll
   for (int u = 0; u < KCH; ++u) {
     const int c = t + kPfThreads * u;
-    koff[u] = (int)((c / NDCH) * krow_g) + (c % NDCH) * 16;
+    constexpr int mask = (NDCH < 16 ? NDCH : 16) - 1;
+    const int r = c / NDCH;
+    koff[u] = (int)(r * krow_g) + (((c % NDCH) ^ (r & mask)) << 4);
   }
 #pragma unroll
   for (int i = 0; i < KPT; ++i) voff[i] = (int)((vk0 + i) * vrow_g) + vdch * 16;
-  u32x4_t kr[KCH], vr[KPT];
-  auto load_tile = [&](int tau) {
-    const int blk = min(max(idx[tau / tpb], 0), nbs - 1);
-    const int64_t page = page_of(p.pages, p.num_pages, (int64_t)off + blk);
-    const int64_t tok0 = page * p.block_size + (int64_t)(tau % tpb) * kPfKeys;
-    const char* kt = kbase + tok0 * krow_g;
-    const char* vt = vbase + tok0 * vrow_g;
+  // First token of the split's tile j.  List and page entries are read with
+  // scalar loads (the tile is the same for the whole workgroup), which do not
+  // wait behind the tile loads in flight.
+  auto tile_tok = [&](int j) -> int64_t {
+    const int tau = t0 + j;
+    const int blk = min(max(ld_const(idx + tau / tpb), 0), nbs - 1);
+    int64_t page = (int64_t)off + blk;
+    if (p.pages) {
+      const int pg = ld_const(p.pages + page);
+      page = (unsigned)pg < (unsigned)p.num_pages ? pg : (pg < 0 ? 0 : p.num_pages - 1);
+    }
+    return page * p.block_size + (int64_t)(tau % tpb) * kPfKeys;
+  };
+  u32x4_t vr[KPT];
+  const int wbase = __builtin_amdgcn_readfirstlane(wave) * kWave * 16;
+  auto load_k = [&](int64_t tok, char* sk) {
+    const char* kt = kbase + tok * krow_g;
 #pragma unroll
-    for (int u = 0; u < KCH; ++u) kr[u] = ld16v(kt + koff[u]);
+    for (int u = 0; u < KCH; ++u)
+      __builtin_amdgcn_global_load_lds((const void*)(kt + koff[u]),
+                                       (__attribute__((address_space(3))) void*)(sk + u * kPfThreads * 16 + wbase),
+                                       16, 0, 0);
+  };
+  auto load_v = [&](int64_t tok) {
+    const char* vt = vbase + tok * vrow_g;
 #pragma unroll
     for (int i = 0; i < KPT; ++i) vr[i] = ld16v(vt + voff[i]);
   };
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int u = 0; u < KCH; ++u) {
-      const int c = t + kPfThreads * u;
-      *reinterpret_cast<u32x4_t*>(s_k + k_off<KROW>(c / NDCH, c % NDCH)) = kr[u];
-    }
-    // V^T: element e of the chunk is dim 8 vdch + e; the KPT keys are
-    // adjacent in vt_pos order, so each dim takes one 4- or 8-byte write.
+  // V^T: element e of the chunk is dim 8 vdch + e; the KPT keys are adjacent
+  // in vt_pos order, so each dim takes one 4- or 8-byte write.
+  auto store_v = [&](char* sv) {
     const int pb = vt_pos(vk0) * 2;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -235,13 +265,29 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
         const uint32_t a = vr[2 * i][w], b = vr[2 * i + 1][w];
         pk[i] = hi ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
       }
-      char* dst = s_v + vt_off(8 * vdch + e, pb);
+      char* dst = sv + vt_off(8 * vdch + e, pb);
       if constexpr (KPT == 4) {
         *reinterpret_cast<uint2*>(dst) = make_uint2(pk[0], pk[1]);
       } else {
         *reinterpret_cast<uint32_t*>(dst) = pk[0];
       }
     }
+  };
+  // S^T for the two 32-key halves of a tile, the two MFMA chains interleaved
+  // over the d slices.
+  auto qk = [&](const char* sk, f32x16_t (&s)[2]) {
+    f32x16_t acc0, acc1;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) { acc0[i] = 0.f; acc1[i] = 0.f; }
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      const u32x4_t a0 = *reinterpret_cast<const u32x4_t*>(sk + k_off<KROW>(q32, 2 * ds + hf));
+      const u32x4_t a1 = *reinterpret_cast<const u32x4_t*>(sk + k_off<KROW>(32 + q32, 2 * ds + hf));
+      acc0 = M::run(a0, qf[ds], acc0);
+      acc1 = M::run(a1, qf[ds], acc1);
+    }
+    s[0] = acc0;
+    s[1] = acc1;
   };
 
   f32x16_t o[DTN];
@@ -252,38 +298,41 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
   float m_run = -INFINITY, l_run = 0.f;
   const float c = p.logit_scale;
 
-  if (t0 < t1) load_tile(t0);
-  for (int tau = t0; tau < t1; ++tau) {
-    __syncthreads();  // the previous tile's operands have been read
-    store_tile();
+  // Prologue: K_0, K_1 and V_0 in LDS, V_1 in registers, S_0.  Every
+  // direct-to-LDS load has completed before the barrier that publishes it.
+  f32x16_t s_cur[2], s_nxt[2];
+  int64_t tok2 = 0;  // first token of tile j+2 at step j
+  if (n > 0) {
+    const int64_t tok0 = tile_tok(0);
+    load_k(tok0, s_k0);
+    const int64_t tok1 = n > 1 ? tile_tok(1) : tok0;
+    if (n > 1) load_k(tok1, s_k1);
+    load_v(tok0);
+    store_v(s_v0);
+    if (n > 1) load_v(tok1);
+    if (n > 2) tok2 = tile_tok(2);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (tau + 1 < t1) load_tile(tau + 1);
+    qk(s_k0, s_cur);
+  }
+  // Tile j: K_j was read by the previous tile's step, V_j and K_{j+1} are in
+  // LDS.  kf / vn: the buffers to fill (K_{j+2}, V_{j+1}); kn / sv: K_{j+1}
+  // and V_j.  Past the end the V store writes stale registers into a buffer
+  // that is never read again, and qk computes an S that is never used.
+  auto step = [&](int j, char* kf, const char* kn, char* vn, const char* sv) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (j + 2 < n) load_k(tok2, kf);
+    store_v(vn);
+    if (j + 2 < n) load_v(tok2);
+    if (j + 3 < n) tok2 = tile_tok(j + 3);
 
-    // S^T for the two 32-key halves of the tile, the two MFMA chains
-    // interleaved over the d slices.  Uniform lists take equal logits (a
-    // select, not a branch).
-    f32x16_t acc0, acc1;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) { acc0[i] = 0.f; acc1[i] = 0.f; }
-#pragma unroll
-    for (int ds = 0; ds < DS; ++ds) {
-      const u32x4_t a0 = *reinterpret_cast<const u32x4_t*>(s_k + k_off<KROW>(q32, 2 * ds + hf));
-      const u32x4_t a1 = *reinterpret_cast<const u32x4_t*>(s_k + k_off<KROW>(32 + q32, 2 * ds + hf));
-      acc0 = M::run(a0, qf[ds], acc0);
-      acc1 = M::run(a1, qf[ds], acc1);
-    }
-    f32x16_t s[2] = {acc0, acc1};
-    if (uni) {  // wave-uniform and rare: equal logits
-#pragma unroll
-      for (int i = 0; i < 16; ++i) { s[0][i] = 0.f; s[1][i] = 0.f; }
-    }
-
-    // Online softmax for query q32 (both lane halves hold the same query).
+    // Online softmax of tile j for query q32 (both lane halves hold it).
     float mx = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][i]);
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[kt][i]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
     // Lazy rescale: the reference point m_run moves only when the tile max
     // exceeds it by more than 2^kLazy (weights stay <= 2^kLazy, exact in fp32
@@ -293,17 +342,6 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
     const bool move = !(m_tile <= m_run + kLazy);  // also true for the first tile (m_run = -inf)
     const float m_new = move ? fmaxf(m_run, m_tile) : m_run;
     const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-    float psum = 0.f;
-    float pv[2][16];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        pv[kt][i] = __builtin_amdgcn_exp2f(fmaf(s[kt][i], c, -m_new));
-        psum += pv[kt][i];
-      }
-    l_run = fmaf(l_run, alpha, psum);
-    m_run = m_new;
     if (__ballot(move)) {  // wave-uniform
 #pragma unroll
       for (int dt = 0; dt < DTN; ++dt)
@@ -311,8 +349,27 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
         for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
     }
 
-    // O^T += V^T P^T over the four 16-key slices; a slice's V^T operands are
-    // read from LDS before its MFMAs.
+    // S_{j+1} (independent of this tile's softmax, so its MFMAs overlap the
+    // exponentials below; the rescale branch comes first so that both are in
+    // one basic block).
+    qk(kn, s_nxt);
+    // P^T slices for the P V product, packed to the MFMA operand type as they
+    // are made; the row sum adds the packed weights (what P V multiplies).
+    float psum = 0.f;
+    u32x4_t pb4[4];
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      float w8[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w8[e] = __builtin_amdgcn_exp2f(fmaf(s_cur[q4 >> 1][8 * (q4 & 1) + e], c, -m_new));
+      pb4[q4] = M::pack(w8);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) psum = dot2_acc<DT>(pb4[q4][w], kOnePair<DT>, psum);
+    }
+    l_run = fmaf(l_run, alpha, psum);
+    m_run = m_new;
+
+    // O^T += V^T P^T over the four 16-key slices.
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
@@ -320,12 +377,18 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
         const int pb = (((kt * 2 + sl) * 2 + hf) << 4);
         u32x4_t va[DTN];
 #pragma unroll
-        for (int dt = 0; dt < DTN; ++dt) va[dt] = *reinterpret_cast<const u32x4_t*>(s_v + vt_off(dt * 32 + q32, pb));
-        const u32x4_t b = M::pack(&pv[kt][8 * sl]);
+        for (int dt = 0; dt < DTN; ++dt) va[dt] = *reinterpret_cast<const u32x4_t*>(sv + vt_off(dt * 32 + q32, pb));
+        const u32x4_t b = pb4[kt * 2 + sl];
 #pragma unroll
         for (int dt = 0; dt < DTN; ++dt) o[dt] = M::run(va[dt], b, o[dt]);
       }
     }
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) s_cur[kt] = s_nxt[kt];
+  };
+  for (int j = 0; j < n; j += 2) {
+    step(j, s_k0, s_k1, s_v1, s_v0);
+    if (j + 1 < n) step(j + 1, s_k1, s_k0, s_v0, s_v1);
   }
 
   // Partial for this split: m and l per row, O^T unnormalised.

@@ -73,6 +73,23 @@ def test_unified_vs_oracle(dev, sq, hq, hkv, d, dtype, nb):
     close(np32(out16), ref, 1e-2)
 
 
+@pytest.mark.parametrize("ntiles", [1, 2, 3, 5, 7])
+def test_short_tile_ranges(dev, ntiles):
+    # 64-token blocks are one key tile each, and this shape gets a single
+    # split, so the kernel walks exactly `ntiles` tiles: the software
+    # pipeline's prologue, odd and even counts and its last two steps.
+    from orthocache_amd import _ops
+
+    bs = 64
+    q, k, v = make(dev, ntiles, 64, 2, 2, 128, torch.bfloat16, seed=30 + ntiles, block=bs)
+    mask = torch.ones(ntiles, dtype=torch.bool, device=dev)
+    c = compact(dev, mask, 2)
+    assert _ops.attend_plan(q, k, v, c.indices, c.num_active, block_size=bs) == ("prefill_mfma", 1)
+    out = _ops.attend(q, k, v, c.indices, c.num_active, block_size=bs, out_dtype=torch.float32)
+    ref = O.attention_active_blocks(np32(q), np32(k), np32(v), range(ntiles), block_size=bs)
+    close(np32(out), ref, 5e-3)
+
+
 def test_matches_decode_kernel(dev):
     # The same bf16 values through both kernel families: fp32 queries take the
     # decode kernel, bf16 queries the MFMA kernel.
