@@ -249,3 +249,30 @@ def test_fused_layer_repeats_deterministically(dev):
     order, n = O.stream_compact_indices(mask)
     np.testing.assert_array_equal(np32(idx[0]).astype(np.int64), order)
     assert int(layer.num_active[0]) == n
+
+
+def test_layer_matches_its_phases(dev):
+    """The fused one-segment layer (oc_decode_layer) and its phases launched
+    as separate calls (oc_score_blocks with logits and mask, then oc_attend
+    from the mask) run the same kernels on the same data: fp32 outputs agree
+    to rounding.  A layer that keeps no block gives zeros."""
+    from orthocache_amd import _ops, workloads
+
+    wl = workloads.c2(dev, seq=16384)
+    sc = _ops.score(wl.k, wl.q)
+    tau, zmax = workloads.calibrate_unified(sc.tau_max[0], sc.zeta, 0.75)
+    layer = _ops.DecodeLayer(wl.q, wl.k, wl.v, tau, zmax, out_dtype=torch.float32)
+    fused = layer.run().clone()
+    score, compact, attend = layer.phases()
+    assert compact is None
+    score()
+    attend()
+    torch.cuda.synchronize()
+    sep = layer.out
+    scale = float(sep.abs().max())
+    assert float((fused - sep).abs().max()) <= 1e-5 * scale
+    none = _ops.DecodeLayer(wl.q, wl.k, wl.v, 1e30, zmax)
+    out = none.run()
+    torch.cuda.synchronize()
+    assert int(none.num_active[0]) == 0
+    assert float(out.float().abs().sum()) == 0.0
