@@ -409,6 +409,10 @@ def run_c3(args, torch, dev):
     torch.cuda.synchronize()
     active = layer.num_active.cpu().numpy()
     us = event_time_us(layer.run, args.steps, torch)
+    # Each phase alone, with the kernels the layer runs (scoring with logits,
+    # mask + compaction, attention + combine).
+    kus = {name: event_time_us(fn, args.kernel_reps, torch)
+           for name, fn in zip(("score", "mask_compact", "attend_and_combine"), layer.phases()) if fn is not None}
     s, hkv, d = wl.k.shape
     hq = wl.q.shape[-2]
     kept = int(active.sum())
@@ -423,7 +427,8 @@ def run_c3(args, torch, dev):
                             "tokens": s, "blocks": s // 512, "retained_blocks": kept,
                             "evict_range": [0.30, 0.95]},
                            {"algorithmic_bytes": total, "layer_gbps": round(gbs, 1),
-                            "layer_frac_of_peak": round(gbs / PEAK_HBM_GBS, 4)})), flush=True)
+                            "layer_frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
+                            "kernels_us": {k: round(v, 2) for k, v in kus.items()}})), flush=True)
 
 
 def run_c5(args, torch, dev):

@@ -481,6 +481,8 @@ __device__ int build_list_offsets(const AttendParams& p, int* s_off, int keep_n)
   return total;
 }
 
+constexpr float kStreamLazy = 8.f;  // log2 headroom before a streaming query's reference moves
+
 // Pieces shared by the streaming forms: a chunk is `chunk` rows of one block
 // and kv head; a lane holds R rows of its slot and VEC columns, and a row
 // slot's online softmax state (m, l, o) for NQ query rows.  KV = false: the
@@ -502,8 +504,10 @@ struct Stream {
   // Chunk buffers in flight: chunk g + NB - 1 is requested before chunk g is
   // consumed (about one workgroup per CU, so registers go to loads in flight;
   // with logits NB = 3 measured best against 2 and 4; keys and values take
-  // twice the registers per chunk).
-  static constexpr int NB = KV ? 2 : 3;
+  // twice the registers per chunk).  Four query rows with logits take two:
+  // 242 VGPRs, two workgroups per CU, where three buffers
+  // needed AGPR spill space and ran one.
+  static constexpr int NB = (KV || NQ == 4) ? 2 : 3;
   static_assert(NQ <= kLogitsMaxQ, "the streaming forms carry at most kLogitsMaxQ queries");
 
   struct State {
@@ -632,30 +636,50 @@ struct Stream {
 
   // Online softmax update with one chunk (all R rows are in the block: the
   // chunk divides the 512-token block).  Uniform lists take equal logits.
+  // Lazy rescale: the reference point m of a query moves only when the
+  // chunk's max exceeds it by more than 2^kStreamLazy (weights stay below
+  // 2^kStreamLazy, exact in fp32); l and o share the reference, so o / l is
+  // unchanged, and most chunks skip the rescale of o.  Weights are v_exp_f32
+  // directly: a weight below 2^-126 of the reference's flushes to zero.
   __device__ __forceinline__ static void consume(State& st, const Buf& b, const Query& qr, int cc, bool uni) {
     float sl[R][NQ];
     logits(b, qr, cc, sl);
+    if (uni) {  // wave-uniform and rare
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int g = 0; g < NQ; ++g) sl[r][g] = 0.f;
+    }
     const uint4 (&vw)[R] = b.vw;
-    float mt[NQ];
+    float mt[NQ], sc[NQ];
+    bool any_move = false;
 #pragma unroll
     for (int g = 0; g < NQ; ++g) {
-      float mx = st.m[g];
+      float mx = sl[0][g];
 #pragma unroll
-      for (int r = 0; r < R; ++r) mx = fmaxf(mx, uni ? 0.f : sl[r][g]);
-      const float sc = (st.m[g] == -INFINITY) ? 0.f : exp2f(st.m[g] - mx);
-      st.l[g] *= sc;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) st.o[g][e] *= sc;
-      mt[g] = mx;
-      st.m[g] = mx;
+      for (int r = 1; r < R; ++r) mx = fmaxf(mx, sl[r][g]);
+      const bool move = !(mx <= st.m[g] + kStreamLazy);  // also true while m = -inf
+      mt[g] = move ? fmaxf(st.m[g], mx) : st.m[g];
+      sc[g] = (st.m[g] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(st.m[g] - mt[g]);
+      any_move |= move;
     }
+    if (__ballot(any_move)) {  // wave-uniform
+#pragma unroll
+      for (int g = 0; g < NQ; ++g) {
+        st.l[g] *= sc[g];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) st.o[g][e] *= sc[g];
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < NQ; ++g) st.m[g] = mt[g];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       float vx[VEC];
       E::unpack(vw[r], vx);
 #pragma unroll
       for (int g = 0; g < NQ; ++g) {
-        const float pw = exp2f((uni ? 0.f : sl[r][g]) - mt[g]);
+        const float pw = __builtin_amdgcn_exp2f(sl[r][g] - mt[g]);
         st.l[g] += pw;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) st.o[g][e] = fmaf(pw, vx[e], st.o[g][e]);
@@ -1167,8 +1191,11 @@ void attend_stream_plan(AttendParams& p) {
     p.splits = (int)(sp < chunks ? sp : chunks);
     return;
   }
+  // Ranges-form workgroups: one per CU, two where the kernel fits two (four
+  // query rows with logits: C3 layer 350.5 -> 345.5 us).
+  const int64_t cap = (p.logits && attend_nq_bucket(p.sq * p.group) == 4) ? 512 : 256;
   const int64_t room = attend_max_items(p) / (kAttendThreads / kWave) - nl;
-  const int64_t g = room < 256 ? room : 256;
+  const int64_t g = room < cap ? room : cap;
   if (g >= 1 && !p.keep) {
     p.stream = kStreamRanges;
     p.splits = (int)g;

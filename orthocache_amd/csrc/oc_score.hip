@@ -59,15 +59,18 @@ __device__ __forceinline__ int find_segment(const int* s_cu, int num_segments, i
 
 // Occupancy target of the logits variants whose registers fit three
 // workgroups per CU without spilling (168 VGPRs): packed dot products
-// (16-bit keys and queries), 32 lanes per row, two query rows.  Measured on
-// the C2 shape (bf16, head_dim 256): 90 us at three workgroups per CU
-// against 97 us at two.
+// (16-bit keys and queries) with 32 lanes per row and two query rows, or bf16
+// with 16 lanes per row and four query rows.  Measured: the C2 shape (bf16,
+// head_dim 256) 90 us at three workgroups per CU against 97 us at two; the C3
+// layer (head_dim 128, four query rows per kv head) 363 us against 377 us.
 // The other bf16 logits variants are held to at least two.  (Some fp16
 // logits variants need more than 256 VGPRs as scheduled and would spill under
 // a floor; they keep the compiler's choice.)
 template <int DT, int LPR, int QDT, int NQL>
 constexpr int score_min_waves() {
-  return (DT != kF32 && QDT == DT && NQL == 2 && LPR == 32) ? 3 : ((NQL > 0 && DT == kBF16) ? 2 : 1);
+  return (DT != kF32 && QDT == DT && ((NQL == 2 && LPR == 32) || (NQL == 4 && LPR == 16 && DT == kBF16)))
+             ? 3
+             : ((NQL > 0 && DT == kBF16) ? 2 : 1);
 }
 
 template <int DT, int LPR, int QDT, int NQL>
@@ -183,21 +186,58 @@ void score_kernel(ScoreParams p) {
     }
   };
 
+  // Sum each row's partial dots over its LPR lanes, then stage them (packed
+  // dot products are scaled once, after the sum).
+  auto reduce_store = [&](auto& part, int l) {
+    constexpr int V = NQL > 0 ? 8 * NQL : LPR;  // (unused without logits)
+    Butterfly<V, V, LPR / 2, LPR>::run(part, cc);
+    const float sc = DOT2 ? p.logit_scale : 1.f;
+    if constexpr (V >= LPR) {
+      constexpr int PER_LANE = V / LPR;
+#pragma unroll
+      for (int u = 0; u < PER_LANE; ++u) {
+        const int idx = cc * PER_LANE + u;
+        s_lg[(64 * (idx / NQL) + l) * NQL + idx % NQL] = part[u] * sc;
+      }
+    } else {
+      // REP = LPR / V lanes hold each complete sum; all of them store it
+      // (same address, same value), which keeps the loop free of branches.
+      constexpr int REP = LPR / V;
+      const int idx = cc / REP;
+      s_lg[(64 * (idx / NQL) + l) * NQL + idx % NQL] = part[0] * sc;
+    }
+  };
+
   auto consume = [&](const uint4 (&r)[8], bool first, int l) {
     constexpr int V = NQL > 0 ? 8 * NQL : 1;
     float part[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) part[i] = 0.f;
-    if constexpr (NQL == 0 || DOT2) {
-      if constexpr (DOT2) {
-        // Packed dot products of the raw key words (two columns each).
+    if constexpr (DOT2) {
+      // Packed dot products of the raw key words (two columns each).
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
+      for (int k = 0; k < 8; ++k)
 #pragma unroll
-          for (int w = 0; w < VEC / 2; ++w)
+        for (int w = 0; w < VEC / 2; ++w)
 #pragma unroll
-            for (int g = 0; g < NQL; ++g) part[k * NQL + g] = dot2_acc<DT>(word_of(r[k], w), lqw[g][w], part[k * NQL + g]);
+          for (int g = 0; g < NQL; ++g) part[k * NQL + g] = dot2_acc<DT>(word_of(r[k], w), lqw[g][w], part[k * NQL + g]);
+    }
+    if constexpr (DOT2 && NQL == 4 && DT == kBF16) {
+      // Four bf16 query rows: the 32 partial sums are reduced and staged
+      // before the statistics, which then widen one column at a time, so the
+      // sums and the widened rows are never live together (162 VGPRs, three
+      // workgroups per CU, at head_dim 128 to 512).
+      reduce_store(part, l);
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) {
+        float x[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = E::get(r[k], c);
+        stats(x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7], first, c);
       }
+      return;
+    }
+    if constexpr (NQL == 0 || DOT2) {
       // Statistics: widen the eight rows at once.
       float x[8][VEC];
 #pragma unroll
@@ -209,26 +249,7 @@ void score_kernel(ScoreParams p) {
 #pragma unroll
       for (int c = 0; c < VEC; ++c) column(r, first, c, part);
     }
-    if constexpr (NQL > 0) {
-      // Sum each row's partial dots over its LPR lanes, then stage them
-      // (packed dot products are scaled once, after the sum).
-      Butterfly<V, V, LPR / 2, LPR>::run(part, cc);
-      const float sc = DOT2 ? p.logit_scale : 1.f;
-      if constexpr (V >= LPR) {
-        constexpr int PER_LANE = V / LPR;
-#pragma unroll
-        for (int u = 0; u < PER_LANE; ++u) {
-          const int idx = cc * PER_LANE + u;
-          s_lg[(64 * (idx / NQL) + l) * NQL + idx % NQL] = part[u] * sc;
-        }
-      } else {
-        // REP = LPR / V lanes hold each complete sum; all of them store it
-        // (same address, same value), which keeps the loop free of branches.
-        constexpr int REP = LPR / V;
-        const int idx = cc / REP;
-        s_lg[(64 * (idx / NQL) + l) * NQL + idx % NQL] = part[0] * sc;
-      }
-    }
+    if constexpr (NQL > 0) reduce_store(part, l);
   };
 
   uint4 ra[8], rb[8];
