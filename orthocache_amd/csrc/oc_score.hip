@@ -57,12 +57,13 @@ __device__ __forceinline__ int find_segment(const int* s_cu, int num_segments, i
   return lo;
 }
 
-// Occupancy target of the logits variants whose registers fit three
+// Occupancy floor of the logits variants whose registers fit three
 // workgroups per CU without spilling (168 VGPRs): packed dot products
 // (16-bit keys and queries) with 32 lanes per row and two query rows, or bf16
 // with 16 lanes per row and four query rows.  Measured: the C2 shape (bf16,
-// head_dim 256) 90 us at three workgroups per CU against 97 us at two; the C3
-// layer (head_dim 128, four query rows per kv head) 363 us against 377 us.
+// head_dim 256) 90 us at three workgroups per CU against 97 us at two (its bf16
+// build now fits four); the C3 layer (head_dim 128, four query rows per kv
+// head) 363 us against 377 us.
 // The other bf16 logits variants are held to at least two.  (Some fp16
 // logits variants need more than 256 VGPRs as scheduled and would spill under
 // a floor; they keep the compiler's choice.)
@@ -222,11 +223,12 @@ void score_kernel(ScoreParams p) {
 #pragma unroll
           for (int g = 0; g < NQL; ++g) part[k * NQL + g] = dot2_acc<DT>(word_of(r[k], w), lqw[g][w], part[k * NQL + g]);
     }
-    if constexpr (DOT2 && NQL == 4 && DT == kBF16) {
-      // Four bf16 query rows: the 32 partial sums are reduced and staged
-      // before the statistics, which then widen one column at a time, so the
-      // sums and the widened rows are never live together (162 VGPRs, three
-      // workgroups per CU, at head_dim 128 to 512).
+    if constexpr (DOT2 && DT == kBF16) {
+      // bf16: the partial sums are reduced and staged before the statistics,
+      // which then widen one column at a time, so the sums and the widened
+      // rows are never live together.  C2's variant (head_dim 256, two query
+      // rows) needs 125 VGPRs, four workgroups per CU, against 136 and three
+      // (scoring 90.8 -> 89.2 us); four query rows 162 against 172-198.
       reduce_store(part, l);
 #pragma unroll
       for (int c = 0; c < VEC; ++c) {
