@@ -1050,6 +1050,109 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
   }
 }
 
+// Ranges form: one workgroup per list (segment, kv head) merges the list's
+// partials for all of its query rows and columns, so the list offsets are
+// scanned once per list (combine_kernel scans them once per query row and 64
+// columns: C3 has 8 times as many workgroups; C3 layer 346 -> 341 us).  The
+// split form keeps combine_kernel: with one list per kv head (C2: 16) this
+// kernel's few workgroups each walk a long chain of loads (C2 layer 108.0 ->
+// 111.3 us).  First the row maxima M of the
+// pieces' references m, then, a batch of partials at a time, the weights
+// exp2(m_j - M) staged in LDS (and l = sum w_j l_j), and each thread
+// accumulates its output elements over the batch in partial order, so the
+// result is deterministic.  An empty list (or only empty pieces, m = -inf)
+// gives zeros.
+constexpr int kListBatch = 256;  // partials whose weights are staged per round
+
+__global__ __launch_bounds__(256) void combine_lists_kernel(AttendParams p) {
+  constexpr int NWS = kAttendThreads / kWave;  // partials per piece (one per wave)
+  constexpr int MQ = kLogitsMaxQ;              // the ranges form carries at most 4 query rows
+  constexpr int EPT = MQ * 512 / 256;          // output elements per thread (head_dim <= 512)
+  __shared__ int s_off[kMaxLists + 1];
+  __shared__ float s_w[kListBatch * MQ];
+  __shared__ float s_red[MQ * 4];
+  const int H = p.num_kv_heads;
+  const int L = blockIdx.x;
+  const int seg = L / H, h = L - seg * H;
+  const int nq = min(p.sq * p.group, MQ);
+  const int D = p.head_dim;
+  const int total = build_list_offsets(p, s_off, -1);
+  const int per = (total + p.splits - 1) / p.splits;
+  const int c0 = s_off[L], c1 = s_off[L + 1];
+  const int fw = c1 > c0 ? c0 / per : 0;
+  const int n = c1 > c0 ? ((c1 - 1) / per - fw + 1) * NWS : 0;
+  const int64_t i0 = ((int64_t)fw + L) * NWS;  // partial j is item i0 + j
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1), wave = t / kWave;
+  auto ml_at = [&](int j, int g) {
+    return *reinterpret_cast<const float2*>(p.part_ml + ((i0 + j) * kQG + g) * 2);
+  };
+
+  float mx[MQ];
+#pragma unroll
+  for (int g = 0; g < MQ; ++g) mx[g] = -INFINITY;
+  for (int j = t; j < n; j += blockDim.x)
+#pragma unroll
+    for (int g = 0; g < MQ; ++g)
+      if (g < nq) mx[g] = fmaxf(mx[g], ml_at(j, g).x);
+#pragma unroll
+  for (int g = 0; g < MQ; ++g) {
+    const float w = wave_max(mx[g]);
+    if (lane == 0) s_red[g * 4 + wave] = w;
+  }
+  __syncthreads();
+  float M[MQ];
+#pragma unroll
+  for (int g = 0; g < MQ; ++g)
+    M[g] = fmaxf(fmaxf(s_red[g * 4], s_red[g * 4 + 1]), fmaxf(s_red[g * 4 + 2], s_red[g * 4 + 3]));
+
+  float lsum[MQ], acc[EPT];
+#pragma unroll
+  for (int g = 0; g < MQ; ++g) lsum[g] = 0.f;
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) acc[k] = 0.f;
+  for (int b0 = 0; b0 < n; b0 += kListBatch) {
+    __syncthreads();  // the previous batch's weights have been used
+    const int j = b0 + t;
+#pragma unroll
+    for (int g = 0; g < MQ; ++g) {
+      float w = 0.f;
+      if (j < n && g < nq) {
+        const float2 ml = ml_at(j, g);
+        w = (ml.x == -INFINITY) ? 0.f : exp2f(ml.x - M[g]);
+        lsum[g] = fmaf(w, ml.y, lsum[g]);
+      }
+      if (t < kListBatch) s_w[t * MQ + g] = w;
+    }
+    __syncthreads();
+    const int nb = min(kListBatch, n - b0);
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const int e = t + 256 * k;
+      if (e < nq * D) {
+        const int g = e / D, d = e - g * D;
+        const float* po = p.part_o + ((i0 + b0) * kQG + g) * D + d;
+        float a = acc[k];
+#pragma unroll 4
+        for (int jj = 0; jj < nb; ++jj) a = fmaf(s_w[jj * MQ + g], po[(int64_t)jj * kQG * D], a);
+        acc[k] = a;
+      }
+    }
+  }
+  block_sum<MQ>(lsum, s_red);
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+    const int e = t + 256 * k;
+    if (e < nq * D) {
+      const int g = e / D, d = e - g * D;
+      const int st = g / p.group, gg = g - st * p.group;
+      const int64_t orow = (int64_t)seg * p.out_seg_stride + (int64_t)st * p.out_tok_stride +
+                           (int64_t)(h * p.group + gg) * p.out_head_stride;
+      store_elt(p.out_dtype, p.out, orow + d, lsum[g] == 0.f ? 0.f : acc[k] / lsum[g]);
+    }
+  }
+}
+
 template <int DT, int LPR, int NQ>
 static hipError_t launch_attend_t(const AttendParams& p, int grid, hipStream_t s) {
   if (p.logits) {
@@ -1215,6 +1318,10 @@ hipError_t launch_attend(const AttendParams& p_in, hipStream_t s) {
       default: return hipErrorInvalidValue;
     }
     if (e != hipSuccess) return e;
+    if (p.stream == kStreamRanges) {
+      hipLaunchKernelGGL(combine_lists_kernel, dim3(p.num_segments * p.num_kv_heads), dim3(256), 0, s, p);
+      return hipGetLastError();
+    }
     const int rows = p.num_segments * p.sq * p.num_kv_heads * p.group;
     const int ndc = (p.head_dim + 63) / 64;
     hipLaunchKernelGGL(combine_kernel, dim3(rows * ndc), dim3(256), 0, s, p);
