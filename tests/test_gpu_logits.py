@@ -261,3 +261,102 @@ def test_streaming_ragged_segments(dev):
         else:
             assert np.all(np32(out_lg)[s] == 0)
         off += n
+
+
+def _rising_keys(dev, q, hkv, nblk, centers, seed):
+    """Keys whose logits against the kv head's (shared) query direction sit
+    around a per-block centre (log2 units) with a spread of +-3: the streaming
+    softmax's reference point must move by less and by more than its 2^8
+    headroom from block to block."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    sq, hq, d = q.shape[-3:]
+    grp = hq // hkv
+    qf = q.float().reshape(-1, hq, d)[0]
+    k = torch.empty(nblk * 512, hkv, d, device=dev)
+    for h in range(hkv):
+        u = qf[h * grp:(h + 1) * grp].mean(0)
+        scale = math.sqrt(d) / LOG2E / float(u.dot(u))
+        t = torch.tensor(centers, device=dev, dtype=torch.float32).repeat_interleave(512)
+        t = t + 3.0 * torch.randn(nblk * 512, generator=g, device=dev)
+        k[:, h] = t[:, None] * scale * u[None, :] + 0.05 * torch.randn(nblk * 512, d, generator=g, device=dev)
+    return k.to(q.dtype)
+
+
+@pytest.mark.parametrize("form", ["split", "ranges"])
+def test_streaming_lazy_rescale_rising_logits(dev, form):
+    """Logit levels that climb block by block, in steps below and above the
+    2^8 headroom of the lazy rescale (and one that falls back), through the
+    scoring-pass logits and the streaming attention, against the oracle."""
+    from orthocache_amd import _ops
+
+    hkv, hq, d = 2, 8, 128
+    centers = [0.0, 2.0, 4.0, 15.0, 16.0, 30.0, 5.0, 31.0, 45.0, 44.0]
+    nblk = len(centers)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(41)
+    nseg = 1 if form == "split" else 2
+    q = (torch.randn(nseg, 1, hq, d, generator=gen, device=dev) * 0.2 + 1.0).to(torch.bfloat16)
+    ks, vs = [], []
+    for s in range(nseg):
+        ks.append(_rising_keys(dev, q[s], hkv, nblk, centers, seed=42 + s))
+        vs.append(torch.randn(nblk * 512, hkv, d, generator=gen, device=dev).to(torch.bfloat16))
+    k, v = torch.cat(ks), torch.cat(vs)
+    keep = [0, 1, 2, 3, 5, 6, 7, 8, 9]  # block 4 evicted
+    m = np.zeros(nblk * nseg, bool)
+    for s in range(nseg):
+        m[[s * nblk + j for j in keep]] = True
+    if form == "split":
+        qq = q[0]
+        c = _ops.mask_compact(num_blocks=nblk, num_kv_heads=hkv, device=dev, mask_in=torch.from_numpy(m).to(dev))
+        sc = _ops.score(k, qq, want_logits=True)
+        kw = dict(out_dtype=torch.float32)
+    else:
+        qq = q
+        cu = torch.tensor([0, nblk, 2 * nblk], dtype=torch.int32, device=dev)
+        c = _ops.mask_compact(num_blocks=nblk * nseg, num_kv_heads=hkv, device=dev, mask_in=torch.from_numpy(m).to(dev),
+                              cu_blocks=cu, num_segments=nseg)
+        sc = _ops.score(k, qq, cu_blocks=cu, num_segments=nseg, want_logits=True)
+        kw = dict(cu_blocks=cu, num_segments=nseg, out_dtype=torch.float32)
+    out = _ops.attend(qq, k, v, c.indices, c.num_active, logits=sc.logits, **kw)
+    torch.cuda.synchronize()
+    lg = np32(sc.logits)
+    assert lg.max() - lg.min() > 60.0  # the designed spread of logit levels is present
+    qn, kn, vn, on = np32(q), np32(k), np32(v), np32(out).reshape(nseg, 1, hq, d)
+    for s in range(nseg):
+        sl = slice(s * nblk * 512, (s + 1) * nblk * 512)
+        ref = O.attention_active_blocks(qn[s], kn[sl], vn[sl], keep)
+        close(on[s], ref, 2e-3)
+
+
+def test_ranges_combine_many_partials(dev):
+    """One list far longer than the others: with four query rows the ranges
+    form cuts all chunks into ~400 ranges, so the long list is merged from
+    640 partials -- more than one batch of staged weights in the per-list
+    combine.  Against the key-reading attention (a different partition) and
+    the oracle."""
+    from orthocache_amd import _ops
+
+    hkv, hq, d = 2, 8, 128
+    seg_blocks = [200, 2]
+    nb = sum(seg_blocks)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(51)
+    k = torch.randn(nb * 512, hkv, d, generator=gen, device=dev).to(torch.bfloat16)
+    v = torch.randn(nb * 512, hkv, d, generator=gen, device=dev).to(torch.bfloat16)
+    q = torch.randn(len(seg_blocks), 1, hq, d, generator=gen, device=dev).to(torch.bfloat16)
+    cu = torch.tensor([0, 200, 202], dtype=torch.int32, device=dev)
+    m = np.zeros(nb, bool)
+    m[:200] = True
+    m[201] = True
+    c = _ops.mask_compact(num_blocks=nb, num_kv_heads=hkv, device=dev, mask_in=torch.from_numpy(m).to(dev),
+                          cu_blocks=cu, num_segments=2)
+    sc = _ops.score(k, q, cu_blocks=cu, num_segments=2, want_logits=True)
+    kw = dict(cu_blocks=cu, num_segments=2, out_dtype=torch.float32)
+    out_lg = _ops.attend(q, k, v, c.indices, c.num_active, logits=sc.logits, **kw)
+    out_k = _ops.attend(q, k, v, c.indices, c.num_active, **kw)
+    torch.cuda.synchronize()
+    close(np32(out_lg), np32(out_k), 1e-5)
+    qn, kn, vn = np32(q), np32(k), np32(v)
+    close(np32(out_lg)[0], O.attention_active_blocks(qn[0], kn[:200 * 512], vn[:200 * 512], range(200)), 2e-3)
+    close(np32(out_lg)[1], O.attention_active_blocks(qn[1], kn[200 * 512:], vn[200 * 512:], [1]), 2e-3)
