@@ -935,7 +935,8 @@ __global__ __launch_bounds__(kAttendThreads) void attend_stream_kernel(AttendPar
   flush(Lc);
 }
 
-// Combine: one workgroup per (output row, 64-wide head_dim slice).  Wave w
+// Combine (per-item and split forms; the ranges form has combine_lists_kernel
+// below): one workgroup per (output row, 64-wide head_dim slice).  Wave w
 // takes the list's items w, w+4, ... in rounds of kCombineBatch items: each
 // lane requests the partial outputs of the round's items for its column and
 // lane u the (m, l) of item u, all before any arithmetic, so one round trip
@@ -951,10 +952,7 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
   __shared__ float s_acc[4 * 64];
   const int nq_total = p.sq * p.group;
   const int nqg = (nq_total + kQG - 1) / kQG;
-  const bool ranges = p.stream == kStreamRanges;
-  int total = 0;
-  if (ranges) total = build_list_offsets(p, s_off, -1);
-  else if (p.stream == kStreamNone && (p.per_head || p.num_segments != 1)) build_item_offsets(p, s_off, nqg);
+  if (p.stream == kStreamNone && (p.per_head || p.num_segments != 1)) build_item_offsets(p, s_off, nqg);
   const int D = p.head_dim;
   const int ndc = (D + 63) / 64;
   int id = blockIdx.x;
@@ -968,31 +966,16 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
   const int qg = qi / kQG, ql = qi - qg * kQG;
   const int list = seg * p.num_kv_heads + h;
   const int H = p.num_kv_heads;
-  // Streaming form: the list's pieces are the workgroups fw..lw whose chunk
-  // ranges meet it (P chunks per workgroup), partial slots fw + L .. lw + L.
-  // Otherwise one partial per (slot, chunk) of the list.
-  constexpr int NWS = kAttendThreads / kWave;  // ranges form: partials per piece (one per wave)
-  int n, fw = 0;
-  if (ranges) {
-    const int per = (total + p.splits - 1) / p.splits;
-    const int c0 = s_off[list], c1 = s_off[list + 1];
-    fw = c1 > c0 ? c0 / per : 0;
-    n = c1 > c0 ? ((c1 - 1) / per - fw + 1) * NWS : 0;
-  } else if (p.stream == kStreamSplit) {
-    n = p.splits;  // one partial per split (empty splits hold m = -inf, l = 0)
-  } else {
-    n = list_count(p, list) * p.nchunk;
-  }
-  // Item of the list's j-th partial, i0 + j * istr in every form: per-item
-  // partials are enumerated head-fastest within the segment for unified
-  // lists and list by list for per-head lists; split partials are
-  // split * Hkv + h; ranges partials ((fw + j / NWS) + L) * NWS + j % NWS,
-  // i.e. (fw + L) * NWS + j.
+  // Split form: one partial per split (empty splits hold m = -inf, l = 0);
+  // per-item form: one partial per (slot, chunk) of the list.
+  const int n = p.stream == kStreamSplit ? p.splits : list_count(p, list) * p.nchunk;
+  // Item of the list's j-th partial, i0 + j * istr: split partials are
+  // split * Hkv + h; per-item partials are enumerated head-fastest within the
+  // segment for unified lists and list by list for per-head lists.
   const bool one_unit = !p.per_head && p.num_segments == 1;
   const int base = (one_unit || p.stream != kStreamNone) ? 0 : s_off[p.per_head ? list : seg];
   int64_t i0, istr;
-  if (ranges) { i0 = ((int64_t)fw + list) * NWS; istr = 1; }
-  else if (p.stream == kStreamSplit) { i0 = h; istr = H; }
+  if (p.stream == kStreamSplit) { i0 = h; istr = H; }
   else if (p.per_head) { i0 = base + qg; istr = nqg; }
   else { i0 = (int64_t)base + (int64_t)qg * H + h; istr = (int64_t)nqg * H; }
   auto item_of = [&](int j) -> int64_t { return i0 + (int64_t)j * istr; };
