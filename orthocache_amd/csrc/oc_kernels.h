@@ -242,15 +242,19 @@ hipError_t launch_attend(const AttendParams& p, hipStream_t s);
 constexpr int kPrefillMinRows = 32;   // query rows per kv head from which the MFMA path is used
 constexpr int kPrefillMaxSplit = 16;
 
-constexpr int kPrefillRows = 128;     // query rows per prefill workgroup (4 waves x 32)
+// Waves per prefill workgroup, one 32-row MFMA tile each: 8 for head_dim 128
+// (each staged K / V^T tile serves 256 query rows), 4 for head_dim 64.
+__host__ __device__ constexpr int prefill_waves(int head_dim) { return head_dim >= 128 ? 8 : 4; }
+__host__ __device__ constexpr int prefill_tile_rows(int head_dim) { return prefill_waves(head_dim) * 32; }
 
 __host__ __device__ inline int prefill_rows(const AttendParams& p) { return p.sq * p.group; }
 __host__ __device__ inline int prefill_qtiles(const AttendParams& p) {
-  return (prefill_rows(p) + kPrefillRows - 1) / kPrefillRows;
+  const int tr = prefill_tile_rows(p.head_dim);
+  return (prefill_rows(p) + tr - 1) / tr;
 }
-// Partial rows per (split, segment, kv head): the query tiles padded to 128.
+// Partial rows per (split, segment, kv head): the query tiles padded to whole tiles.
 __host__ __device__ inline int64_t prefill_rows_pad(const AttendParams& p) {
-  return (int64_t)prefill_qtiles(p) * kPrefillRows;
+  return (int64_t)prefill_qtiles(p) * prefill_tile_rows(p.head_dim);
 }
 
 bool prefill_supported(int kv_dtype, int q_dtype, int head_dim, int nq_rows, int block_size);

@@ -8,8 +8,10 @@
 // has enough query rows (query tokens x heads of its group) that Q K^T and P V
 // are dense contractions (chunked prefill).
 //
-// Work decomposition: a workgroup (4 waves) takes 128 query rows of one
-// (segment, kv head) and a contiguous range of the list's 64-key tiles (the
+// Work decomposition: a workgroup (8 waves for head_dim 128, 4 for 64; 32
+// query rows per wave, so each staged K / V^T tile serves 256 or 128 rows)
+// takes one query tile of a (segment, kv head) and a contiguous range of the
+// list's 64-key tiles (the
 // tile range is split `nsplit` ways so the grid fills the chip); it writes a
 // partial (m, l, O) per row and prefill_combine_kernel merges the splits.
 //
@@ -41,10 +43,8 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kPfWaves = 4;
-constexpr int kPfThreads = kPfWaves * kWave;
-constexpr int kPfRows = kPrefillRows;
-static_assert(kPfRows == kPfWaves * 32, "one 32-row MFMA tile per wave");
+constexpr int kPfMaxThreads = 8 * kWave;  // largest prefill workgroup (head_dim 128)
+static_assert(prefill_waves(128) * kWave == kPfMaxThreads, "workgroup size");
 constexpr int kPfKeys = 64;             // keys per tile
 constexpr float kLazy = 8.f;            // log2 headroom before the softmax reference moves
 // (1, 1) as a packed pair of the operand type, for row sums by dot2.
@@ -120,13 +120,15 @@ int64_t prefill_partial_floats(const AttendParams& p) {
 }
 
 template <int DT, int D>
-__global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendParams p) {
+__global__ __launch_bounds__(kPfMaxThreads, 2) void attend_prefill_kernel(AttendParams p) {
   using M = Mma<DT>;
+  constexpr int kPfThreads = prefill_waves(D) * kWave;
+  constexpr int kPfRows = prefill_tile_rows(D);
   constexpr int DS = D / 16;                 // d slices of Q K^T
   constexpr int DTN = D / 32;                // 32-row d tiles of O^T
   constexpr int KROW = D * 2;                // bytes per K row in LDS
   constexpr int KCH = kPfKeys * D / 8 / kPfThreads;  // 16-byte K chunks per thread
-  constexpr int KPT = D / 32;                // keys per thread in the V transpose (2 or 4)
+  constexpr int KPT = kPfKeys * (D / 8) / kPfThreads;  // keys per thread in the V transpose (2)
   constexpr int NDCH = D / 8;                // 16-byte chunks per row
   static_assert(KCH >= 1 && (KPT == 2 || KPT == 4), "unsupported head_dim");
 
@@ -194,15 +196,16 @@ __global__ __launch_bounds__(kPfThreads, 2) void attend_prefill_kernel(AttendPar
   const char* kbase = reinterpret_cast<const char*>(p.k) + (int64_t)h * p.k_head_stride * 2;
   const char* vbase = reinterpret_cast<const char*>(p.v) + (int64_t)h * p.v_head_stride * 2;
 
-  // This thread's share of a tile: K chunks c = t + 256 u, loaded straight
+  // This thread's share of a tile: K chunks c = t + kPfThreads u, loaded straight
   // into LDS (lane l of a wave writes 16 bytes at the instruction's base +
   // 16 l), so LDS chunk c -- row c / NDCH, swizzled position c % NDCH -- is
   // fetched from the global chunk the swizzle puts there; V keys
   // vk0 .. vk0 + KPT - 1 at chunk vdch, through registers for the transpose.
-  // Lane -> (16-byte chunk, key group) of the V transpose.  For head_dim 128
-  // the 16 lanes of an LDS write phase cover 8 dims x 2 key groups whose
-  // positions differ in the 8-byte half of a block, so the writes spread over
-  // all banks; each key row is still read as 256 contiguous bytes.
+  // Lane -> (16-byte chunk, key group) of the V transpose (two keys per
+  // thread).  For head_dim 128 the 16 lanes of an LDS write phase cover 8
+  // dims x 2 key groups four keys apart, which sit in different 16-byte
+  // blocks of a V^T row, so the writes spread over the banks; each key row is
+  // still read as 256 contiguous bytes.
   int vdch, vgrp;
   if constexpr (NDCH == 16) {
     vdch = (t & 7) | (((t >> 4) & 1) << 3);
@@ -481,7 +484,7 @@ static hipError_t launch_prefill_t(const AttendParams& p, hipStream_t s) {
   const int nqt = prefill_qtiles(p);
   const int64_t grid = (int64_t)p.num_segments * p.num_kv_heads * nqt * p.nsplit;
   if (grid > 0) {
-    hipLaunchKernelGGL((attend_prefill_kernel<DT, D>), dim3((unsigned)grid), dim3(kPfThreads), 0, s, p);
+    hipLaunchKernelGGL((attend_prefill_kernel<DT, D>), dim3((unsigned)grid), dim3(prefill_waves(D) * kWave), 0, s, p);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

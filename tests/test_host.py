@@ -133,7 +133,7 @@ def _plan_args(sq, hq, hkv, d, dtype, block=512, nb=256, q_dtype=None):
 
 
 @pytest.mark.parametrize("sq,hq,hkv,d,dt,block,qdt,expect", [
-    (512, 8, 8, 128, 1, 512, None, (1, 16)),   # C4: 32 (head, 128-row) tiles x 16 splits
+    (512, 8, 8, 128, 1, 512, None, (1, 16)),   # C4: 16 (head, 256-row) tiles x 16 splits
     (512, 8, 8, 128, 2, 512, None, (1, 16)),   # fp16
     (512, 8, 8, 64, 1, 512, None, (1, 16)),
     (16, 32, 8, 128, 1, 512, None, (1, 16)),   # 4 x 16 = 64 rows per kv head, one query tile
