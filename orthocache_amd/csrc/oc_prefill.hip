@@ -202,14 +202,16 @@ __global__ __launch_bounds__(kPfMaxThreads, 2) void attend_prefill_kernel(Attend
   // fetched from the global chunk the swizzle puts there; V keys
   // vk0 .. vk0 + KPT - 1 at chunk vdch, through registers for the transpose.
   // Lane -> (16-byte chunk, key group) of the V transpose (two keys per
-  // thread).  For head_dim 128 the 16 lanes of an LDS write phase cover 8
-  // dims x 2 key groups four keys apart, which sit in different 16-byte
-  // blocks of a V^T row, so the writes spread over the banks; each key row is
-  // still read as 256 contiguous bytes.
+  // thread, one 4-byte write per dim).  For head_dim 128 the 32 lanes of an
+  // LDS write phase cover 8 dims (8 rows of V^T, whose swizzles differ) x the
+  // 4 key pairs of one 16-byte block position, i.e. 32 distinct banks; a
+  // wave still reads whole 256-byte key rows.  (The previous map put only 8
+  // banks under a phase: 16% bank-conflict cycles, no measurable time.)
   int vdch, vgrp;
   if constexpr (NDCH == 16) {
-    vdch = (t & 7) | (((t >> 4) & 1) << 3);
-    vgrp = (t >> 6) * 4 + ((t >> 3) & 1) * 2 + ((t >> 5) & 1);
+    static_assert(kPfThreads == 512 && KPT == 2, "lane map for 512 threads, two keys each");
+    vdch = (t & 7) | (((t >> 5) & 1) << 3);
+    vgrp = ((t >> 3) & 1) | (((t >> 6) & 1) << 1) | (((t >> 4) & 1) << 2) | (((t >> 7) & 3) << 3);
   } else {
     vdch = t % NDCH;
     vgrp = t / NDCH;
