@@ -468,6 +468,10 @@ __global__ __launch_bounds__(256) void bound_kernel(BoundParams p) {
   const float* dcrow = p.dc + ((int64_t)min(brow, nb - 1) * H + h) * D;
   const float eac = p.e_ac[(int64_t)min(brow, nb - 1) * H + h];
 
+  // Reciprocals instead of divisions in the hot loop and the epilogue (a
+  // divide is a ten-instruction sequence; the products differ from the
+  // quotients by at most one rounding).
+  constexpr float kInv = 1.f / kSqrt512;
   const int half = (D + 1) / 2;
   const int d0 = hf * half;
   const int d1 = min(d0 + half, D);
@@ -499,7 +503,7 @@ __global__ __launch_bounds__(256) void bound_kernel(BoundParams p) {
         const float4 kv = *reinterpret_cast<const float4*>(dcrow + dd);
         const float kvv[4] = {kv.x, kv.y, kv.z, kv.w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) kb[j + e] = d < d1 ? kvv[e] / kSqrt512 : 0.f;  // kbar, spectral_energy.py:166
+        for (int e = 0; e < 4; ++e) kb[j + e] = d < d1 ? kvv[e] * kInv : 0.f;  // kbar, spectral_energy.py:166
       }
     } else {
 #pragma unroll
@@ -510,7 +514,7 @@ __global__ __launch_bounds__(256) void bound_kernel(BoundParams p) {
         const float qv = EQ::load1(p.q, qoff + dd);
         const float kv = dcrow[dd];
         qa[j] = ok ? qv : 0.f;
-        kb[j] = ok ? kv / kSqrt512 : 0.f;  // kbar, spectral_energy.py:166
+        kb[j] = ok ? kv * kInv : 0.f;  // kbar, spectral_energy.py:166
       }
     }
 #pragma unroll
@@ -526,7 +530,7 @@ __global__ __launch_bounds__(256) void bound_kernel(BoundParams p) {
   qq += __shfl_xor(qq, 32, kWave);  // full squared norm of query row r
 
   // tau_j(q) = q.kbar/sqrt(d) + ||q|| sqrt(E_AC)/sqrt(d) (spectral_energy.py:170-176).
-  const float sqrt_d = sqrtf((float)D);
+  const float inv_sqrt_d = 1.f / sqrtf((float)D);
   const float sqrt_eac = sqrtf(eac);
   const int b = bt * kBoundBT + wb * 32 + r;
   float m = -INFINITY;
@@ -536,7 +540,7 @@ __global__ __launch_bounds__(256) void bound_kernel(BoundParams p) {
     const float qn = __shfl(qq, rr, kWave);
     const int qi = qt * kBoundQT + wq * 32 + rr;
     if (qi < nq && b < nb) {
-      const float bound = acc[i] / sqrt_d + (sqrtf(qn) * sqrt_eac) / sqrt_d;
+      const float bound = acc[i] * inv_sqrt_d + (sqrtf(qn) * sqrt_eac) * inv_sqrt_d;
       if (p.bounds) p.bounds[((int64_t)qi * nb + b) * H + h] = bound;
       m = nanmax(m, bound);
     }
