@@ -394,7 +394,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_decode_kernel(AttendPar
         E::unpack(vw[r], vx);
 #pragma unroll
         for (int g = 0; g < NQ; ++g) {
-          const float pw = exp2f(sl[r][g] - m[g]);
+          const float pw = __builtin_amdgcn_exp2f(sl[r][g] - m[g]);  // v_exp_f32; below 2^-126 flushes to 0
           l[g] += pw;
 #pragma unroll
           for (int e = 0; e < VEC; ++e) o[g][e] = fmaf(pw, vx[e], o[g][e]);
