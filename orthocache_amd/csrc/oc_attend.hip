@@ -943,9 +943,12 @@ __global__ __launch_bounds__(kAttendThreads) void attend_stream_kernel(AttendPar
 // serves a round (lists of up to 4 * kCombineBatch partials take one).
 // Within a wave the rounds merge online (running max, rescaled sums); the
 // four waves merge through LDS.  The order is fixed, so the result is
-// deterministic.
-constexpr int kCombineBatch = 32;  // items per wave per round (lanes 0..31 hold their m, l)
-
+// deterministic.  kCombineBatch is 32 for per-item lists (lanes 0..31 hold
+// their m, l); the split form, whose partial count is known on the host,
+// takes the smallest batch that covers its splits in one round, so a wave
+// does not issue clamped duplicate loads (C2, 16 splits: batch 4, layer
+// 108.0 -> 106.6 us).
+template <int kCombineBatch>
 __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
   __shared__ int s_off[kMaxLists + 1];
   __shared__ float s_ml[2 * 4];
@@ -1136,6 +1139,16 @@ __global__ __launch_bounds__(256) void combine_lists_kernel(AttendParams p) {
   }
 }
 
+// Row-wise combine with its batch: one round of 4 x batch partials covers the
+// split form's `splits`; per-item lists take 32.
+static void launch_combine(const AttendParams& p, dim3 grid, hipStream_t s) {
+  const int n = p.stream == kStreamSplit ? p.splits : 1 << 30;
+  if (n <= 16) hipLaunchKernelGGL(combine_kernel<4>, grid, dim3(256), 0, s, p);
+  else if (n <= 32) hipLaunchKernelGGL(combine_kernel<8>, grid, dim3(256), 0, s, p);
+  else if (n <= 64) hipLaunchKernelGGL(combine_kernel<16>, grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL(combine_kernel<32>, grid, dim3(256), 0, s, p);
+}
+
 template <int DT, int LPR, int NQ>
 static hipError_t launch_attend_t(const AttendParams& p, int grid, hipStream_t s) {
   if (p.logits) {
@@ -1307,7 +1320,7 @@ hipError_t launch_attend(const AttendParams& p_in, hipStream_t s) {
     }
     const int rows = p.num_segments * p.sq * p.num_kv_heads * p.group;
     const int ndc = (p.head_dim + 63) / 64;
-    hipLaunchKernelGGL(combine_kernel, dim3(rows * ndc), dim3(256), 0, s, p);
+    launch_combine(p, dim3(rows * ndc), s);
     return hipGetLastError();
   }
   const int64_t max_items = attend_max_items(p);
@@ -1325,7 +1338,7 @@ hipError_t launch_attend(const AttendParams& p_in, hipStream_t s) {
   const int rows = p.num_segments * p.sq * p.num_kv_heads * p.group;
   if (rows == 0) return hipSuccess;
   const int ndc = (p.head_dim + 63) / 64;
-  hipLaunchKernelGGL(combine_kernel, dim3(rows * ndc), dim3(256), 0, s, p);
+  launch_combine(p, dim3(rows * ndc), s);
   return hipGetLastError();
 }
 
