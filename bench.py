@@ -216,7 +216,7 @@ def main():
     # What this build's kernels move: with scoring-pass logits the scoring
     # kernel also writes the fp32 logits of every key row, and the attention
     # reads the retained values and logits instead of keys and values.
-    logits = _ops.layer_uses_logits(wl.k.dtype, d, nq)
+    logits = _ops.layer_uses_logits(wl.k.dtype, d, nq, wl.q.dtype)
     nqp = _ops.logits_nq_pad(nq)
     logit_bytes = nb * hkv * 512 * nqp * 4 if logits else 0
     score_bytes = s * hkv * d * esz + q_bytes + nb * hkv * 8 + logit_bytes

@@ -130,10 +130,16 @@ def _set_thresholds(a, tau, zeta_max, device):
     return keep
 
 
-def layer_uses_logits(kv_dtype: torch.dtype, head_dim: int, nq: int) -> bool:
+def layer_uses_logits(kv_dtype: torch.dtype, head_dim: int, nq: int,
+                      q_dtype: torch.dtype = torch.bfloat16) -> bool:
     """Whether oc_decode_layer forms the logits in its scoring pass (the
-    condition of the library's score_logits_supported): 1..4 query rows per kv
-    head and at most 64 lanes of 16 bytes per key row."""
+    library's layer_uses_logits): 1..4 query rows per kv head and at most 64
+    lanes of 16 bytes per key row, except fp16 keys with one row at head_dim
+    256 or with fp32 queries and 3-4 rows at head_dim 128, where the layer is
+    faster with the attention reading the keys."""
+    if kv_dtype == torch.float16 and ((head_dim == 256 and nq == 1) or
+                                      (q_dtype == torch.float32 and head_dim == 128 and nq > 2)):
+        return False
     lanes = head_dim * torch.empty((), dtype=kv_dtype).element_size() // 16
     return 1 <= nq <= LOGITS_QUERY_LIMIT and lanes <= 64
 
@@ -566,7 +572,7 @@ class DecodeLayer:
         # The fused layer forms the attention logits in its scoring pass when
         # it can; the phases do the same, so each phase times the layer's kernel.
         self._phase_logits = None
-        if layer_uses_logits(self.k.dtype, a.head_dim, a.sq * a.group):
+        if layer_uses_logits(self.k.dtype, a.head_dim, a.sq * a.group, self.q.dtype):
             self._phase_logits = torch.empty((a.total_blocks, a.num_kv_heads, BLOCK, logits_nq_pad(a.sq * a.group)),
                                              dtype=torch.float32, device=self.device)
             sa.logits = ptr(self._phase_logits)

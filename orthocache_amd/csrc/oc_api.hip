@@ -335,9 +335,17 @@ bool layer_uses_keep(const oc_layer_args* a) {
 }
 
 // True when the layer's scoring pass also writes the attention logits (the
-// attention then reads values only).
+// attention then reads values only).  fp16 keys with one query row at
+// head_dim 256, or with fp32 queries and 3-4 rows at head_dim 128, are left
+// out: those logit variants of the scoring kernel hold one wave per SIMD, and
+// the layer measured faster with the attention reading the keys itself
+// (150.7 -> 106.4 us and 74.0 -> 45.4 us for 64K tokens on one MI355X).
 bool layer_uses_logits(const oc_layer_args* a) {
-  return oc::score_logits_supported(a->kv_dtype, a->head_dim, a->sq * a->group);
+  const int nq = a->sq * a->group;
+  if (a->kv_dtype == OC_F16 &&
+      ((a->head_dim == 256 && nq == 1) || (a->q_dtype == OC_F32 && a->head_dim == 128 && nq > 2)))
+    return false;
+  return oc::score_logits_supported(a->kv_dtype, a->head_dim, nq);
 }
 
 // Workspace: [tau_max | zeta | indices | num_active | keep | logits | attention partials].

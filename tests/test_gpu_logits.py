@@ -155,7 +155,7 @@ def test_decode_layer_uses_logits_and_matches(dev):
     k = workloads.make_keys(nb, hkv, d, seed=31, device=dev, noise_blocks=2)
     v = workloads.make_values(nb * 512, hkv, d, seed=32, device=dev)
     q = workloads.make_queries((1, hq, d), d, seed=33, device=dev)
-    assert _ops.layer_uses_logits(k.dtype, d, hq // hkv)
+    assert _ops.layer_uses_logits(k.dtype, d, hq // hkv, q.dtype)
     sc = _ops.score(k, q)
     tau, zmax = workloads.calibrate_unified(sc.tau_max[0], sc.zeta, evict=0.75)
     layer = _ops.DecodeLayer(q, k, v, tau, zmax, out_dtype=torch.float32)
@@ -166,6 +166,44 @@ def test_decode_layer_uses_logits_and_matches(dev):
     torch.cuda.synchronize()
     assert torch.equal(layer.indices, c.indices) and torch.equal(layer.num_active, c.num_active)
     close(np32(out), np32(ref), 1e-5)
+
+
+@pytest.mark.parametrize("hkv,hq,d,qdt", [
+    (4, 4, 256, torch.float16),    # fp16, one row at head_dim 256
+    (4, 4, 256, torch.float32),    # fp32 queries over fp16 keys
+    (2, 8, 128, torch.float32),    # fp32 queries, four rows at head_dim 128
+])
+def test_decode_layer_fp16_without_logits(dev, hkv, hq, d, qdt):
+    """fp16 shapes whose layer reads the keys in the attention instead of
+    scoring-pass logits: same mask and list as the separate calls, attention
+    within fp32 rounding, and the float64 oracle within the decode tolerance."""
+    from orthocache_amd import _ops, workloads
+
+    nb = 10
+    k = workloads.make_keys(nb, hkv, d, seed=41, device=dev, dtype=torch.float16, noise_blocks=2)
+    v = workloads.make_values(nb * 512, hkv, d, seed=42, device=dev, dtype=torch.float16)
+    q = workloads.make_queries((1, hq, d), d, seed=43, device=dev, dtype=qdt)
+    assert not _ops.layer_uses_logits(k.dtype, d, hq // hkv, q.dtype)
+    sc = _ops.score(k, q)
+    tau, zmax = workloads.calibrate_unified(sc.tau_max[0], sc.zeta, evict=0.6)
+    layer = _ops.DecodeLayer(q, k, v, tau, zmax, out_dtype=torch.float32)
+    out = layer.run()
+    c = _ops.mask_compact(num_blocks=nb, num_kv_heads=hkv, device=dev, tau_max=sc.tau_max, zeta=sc.zeta,
+                          tau=tau, zeta_max=zmax)
+    ref = _ops.attend(q, k, v, c.indices, c.num_active, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(layer.indices, c.indices) and torch.equal(layer.num_active, c.num_active)
+    close(np32(out), np32(ref), 1e-5)
+    n = int(c.num_active[0])
+    act = layer.indices[:n].cpu().numpy()
+    close(np32(out), O.attention_active_blocks(np32(q), np32(k), np32(v), act), 2e-3)
+    fused = out.clone()
+    score, compact, attend = layer.phases()
+    assert compact is None
+    score()
+    attend()
+    torch.cuda.synchronize()
+    assert float((fused - layer.out).abs().max()) <= 1e-5 * float(fused.abs().max())
 
 
 @pytest.mark.parametrize("nb,hkv,hq,d,keep", [

@@ -38,7 +38,7 @@ def test_score_mask_matches_compaction(dev, hkv, hq, d):
     q = workloads.make_queries((1, hq, d), d, seed=7, device=dev)
     plain = _ops.score(k, q)
     tau, zmax = workloads.calibrate_unified(plain.tau_max[0], plain.zeta, evict=0.5)
-    res = _ops.score(k, q, gate=(tau, zmax), want_logits=_ops.layer_uses_logits(k.dtype, d, hq // hkv))
+    res = _ops.score(k, q, gate=(tau, zmax), want_logits=_ops.layer_uses_logits(k.dtype, d, hq // hkv, q.dtype))
     c = _ops.mask_compact(num_blocks=nb, num_kv_heads=hkv, device=dev, tau_max=res.tau_max, zeta=res.zeta,
                           tau=tau, zeta_max=zmax, want_mask=True)
     torch.cuda.synchronize()

@@ -197,3 +197,34 @@ def test_scoring_identity_fp32_cancellation_free():
     _, lo32, _, _ = _kernel_band_identity(blk.astype(np.float32))
     _, lo, _, _ = O.spectral_bands(blk.reshape(512, 1, 64).astype(np.float64))
     np.testing.assert_allclose(lo32, lo[0, 0], rtol=1e-4)
+
+
+@pytest.mark.parametrize("kv", ["bf16", "f16"])
+@pytest.mark.parametrize("qf32", [False, True])
+@pytest.mark.parametrize("d,nq", [(64, 1), (128, 1), (128, 2), (128, 3), (128, 4), (256, 1), (256, 2),
+                                  (256, 4), (512, 1), (128, 5)])
+def test_layer_logits_choice_matches_library(lib, kv, qf32, d, nq):
+    """_ops.layer_uses_logits restates the library's choice: the layer
+    workspace exceeds the cached layer's (which never forms logits) by the
+    logits buffer exactly when the scoring pass writes them."""
+    import torch
+
+    from orthocache_amd import _native as N, _ops
+
+    kdt = torch.bfloat16 if kv == "bf16" else torch.float16
+    qdt = torch.float32 if qf32 else kdt
+    nb, hkv = 24, 2
+    a = N.LayerArgs()
+    a.q = 256; a.q_dtype = N.dtype_code(qdt); a.q_tok_stride = nq * hkv * d; a.q_head_stride = d
+    a.k = 256; a.v = 256; a.kv_dtype = N.dtype_code(kdt)
+    a.k_tok_stride = a.v_tok_stride = hkv * d; a.k_head_stride = a.v_head_stride = d
+    a.head_dim = d; a.num_kv_heads = hkv; a.group = nq; a.sq = 1; a.total_blocks = nb; a.num_segments = 1
+    a.out = 256; a.out_dtype = N.dtype_code(qdt); a.out_tok_stride = nq * hkv * d; a.out_head_stride = d
+    full = int(lib.oc_decode_layer_workspace_size(C.byref(a)))
+    cached = int(lib.oc_decode_layer_cached_workspace_size(C.byref(a)))
+    assert full > 0 and cached > 0
+    logit_bytes = -(-nb * hkv * 512 * _ops.logits_nq_pad(nq) * 4 // 256) * 256
+    uses = _ops.layer_uses_logits(kdt, d, nq, qdt)
+    assert full - cached == (logit_bytes if uses else 0)
+    if kv == "bf16" and nq <= 4 and d <= 256:
+        assert uses
