@@ -143,6 +143,15 @@ __device__ __forceinline__ uint4 ld16_nt(const void* p) {
   return make_uint4(w.x, w.y, w.z, w.w);
 }
 
+// 16-byte non-temporal store for data the kernel writes once and another
+// launch reads (the scoring pass's logits): the line is not kept dirty in the
+// writer's L2.  C2 decode layer 107.0-107.8 -> 105.5-106.0 us.
+__device__ __forceinline__ void st16_nt(void* p, float4 v) {
+  typedef float v4f __attribute__((ext_vector_type(4)));
+  const v4f w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<v4f*>(p));
+}
+
 // -------------------------------------------------------------- reductions
 // jnp.max semantics: NaN in either operand propagates.
 __device__ __forceinline__ float nanmax(float a, float b) { return (a > b || a != a) ? a : b; }

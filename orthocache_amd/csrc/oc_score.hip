@@ -314,7 +314,7 @@ void score_kernel(ScoreParams p) {
     float* dst = p.logits + (int64_t)tile * kBlock * NQL;
 #pragma unroll
     for (int i = 4 * t; i < kBlock * NQL; i += 4 * 256)
-      *reinterpret_cast<float4*>(dst + i) = *reinterpret_cast<const float4*>(s_lg + i);
+      st16_nt(dst + i, *reinterpret_cast<const float4*>(s_lg + i));
   }
 
   // Per column: merge the NSLOT partial (mean, M2) pairs (equal counts NLO).
