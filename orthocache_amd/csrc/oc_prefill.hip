@@ -401,8 +401,8 @@ __global__ __launch_bounds__(kPfMaxThreads, 2) void attend_prefill_kernel(Attend
   const int64_t rows_pad = (int64_t)nqt * kPfRows;
   const int64_t slab = ((int64_t)(split * p.num_segments + seg) * p.num_kv_heads + h);
   if (hf == 0) {
-    p.part_ml[(slab * rows_pad + row) * 2] = m_run;
-    p.part_ml[(slab * rows_pad + row) * 2 + 1] = l_tot;
+    st4_nt(p.part_ml + (slab * rows_pad + row) * 2, m_run);
+    st4_nt(p.part_ml + (slab * rows_pad + row) * 2 + 1, l_tot);
   }
   float* po = p.part_o + slab * D * rows_pad + row;
 #pragma unroll
@@ -410,7 +410,7 @@ __global__ __launch_bounds__(kPfMaxThreads, 2) void attend_prefill_kernel(Attend
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int d = dt * 32 + 8 * (i >> 2) + 4 * hf + (i & 3);
-      po[(int64_t)d * rows_pad] = o[dt][i];
+      st4_nt(po + (int64_t)d * rows_pad, o[dt][i]);
     }
 }
 
