@@ -206,6 +206,47 @@ def test_decode_layer_fp16_without_logits(dev, hkv, hq, d, qdt):
     assert float((fused - layer.out).abs().max()) <= 1e-5 * float(fused.abs().max())
 
 
+@pytest.mark.parametrize("qdt", [torch.float16, torch.float32])
+def test_ragged_decode_layer_fp16(dev, qdt):
+    """A ragged fp16 batch through the fused layer: with fp32 queries (four
+    rows at head_dim 128) the layer skips scoring-pass logits and the ranges
+    attention reads the keys; with fp16 queries it uses the logits.  Lists
+    match the oracle's mask and compaction exactly, attention the float64
+    oracle within the decode tolerance."""
+    from orthocache_amd import _ops, varlen, workloads
+
+    hkv, hq, d = 2, 8, 128
+    lens = [3 * 512, 512, 4 * 512]
+    cu = np.concatenate([[0], np.cumsum(lens)]) // 512
+    nb = int(cu[-1])
+    k = workloads.make_keys(nb, hkv, d, seed=61, device=dev, dtype=torch.float16, noise_blocks=2)
+    v = workloads.make_values(nb * 512, hkv, d, seed=62, device=dev, dtype=torch.float16)
+    q = workloads.make_queries((len(lens), 1, hq, d), d, seed=63, device=dev, dtype=qdt)
+    assert _ops.layer_uses_logits(k.dtype, d, hq // hkv, q.dtype) == (qdt == torch.float16)
+    cu_seqlens = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=dev)
+    tm, z = varlen.score_varlen(q, k, cu_seqlens)
+    taus, zmaxs = [], []
+    for s in range(len(lens)):
+        t, zm = workloads.calibrate_unified(tm[cu[s]:cu[s + 1]], z[cu[s]:cu[s + 1]], 0.5)
+        taus.append(t)
+        zmaxs.append(zm)
+    tau_t = torch.tensor(taus, dtype=torch.float32, device=dev)
+    zmax_t = torch.tensor(zmaxs, dtype=torch.float32, device=dev)
+    out, meta = varlen.orthocache_decode_varlen(q, k, v, cu_seqlens, tau_t, zmax_t, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    idx = np32(meta["indices"]).astype(np.int64)
+    tmn, zn = np32(meta["tau_max"]), np32(meta["zeta"])
+    for s in range(len(lens)):
+        lo, hi = cu[s], cu[s + 1]
+        mask = O.mask_from_scores(tmn[lo:hi], zn[lo:hi], taus[s], zmaxs[s])
+        order, n = O.stream_compact_indices(mask)
+        np.testing.assert_array_equal(idx[lo:hi], order)
+        assert int(meta["num_active"][s]) == n
+        ref = O.attention_active_blocks(np32(q[s]), np32(k[lo * 512:hi * 512]), np32(v[lo * 512:hi * 512]),
+                                        order[:n])
+        close(np32(out[s]), ref, 2e-3)
+
+
 @pytest.mark.parametrize("nb,hkv,hq,d,keep", [
     (1, 1, 1, 128, "all"), (2, 16, 32, 256, "all"), (13, 16, 32, 256, "some"), (128, 16, 32, 256, "some"),
     (7, 8, 32, 128, "none"), (40, 2, 8, 64, "some"), (300, 4, 4, 128, "some")])
