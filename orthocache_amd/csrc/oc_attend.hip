@@ -818,11 +818,13 @@ __global__ __launch_bounds__(kAttendThreads) void attend_split_kernel(AttendPara
 // [w P, (w + 1) P) of it, P = ceil(total / grid), so every workgroup streams
 // the same number of chunks whatever the lists' lengths.  It keeps the slot
 // states while the chunks belong to one list; when the list changes (and at
-// the end) each wave merges its slots with shuffles and writes its own
-// partial, slot (w + L) * NWAVE + wave: no barrier and no wait on the chunks
-// in flight inside the loop.  Slots are distinct for distinct (w, L) because
-// ranges are monotone in w; the combine finds a list's pieces from the same
-// offsets.  List entries and offsets are read wave-uniformly (readfirstlane,
+// the end) each wave merges its slots with shuffles, the waves merge through
+// LDS behind LDS-only barriers (the chunks in flight are not waited for; all
+// waves walk the same chunks, so they reach a list change together), and the
+// workgroup writes one partial, slot w + L.  Slots are distinct for distinct
+// (w, L) because ranges are monotone in w; the combine finds a list's pieces
+// from the same offsets.  (One partial per wave instead, merged by the
+// combine: C3 combine 12.3 us.)  List entries and offsets are read wave-uniformly (readfirstlane,
 // constant-address loads), so the next chunk's list entry is a scalar load
 // that does not wait for the vector loads in flight.
 template <int DT, int LPR, int NQ, bool KV, int QDT>
@@ -830,6 +832,8 @@ __global__ __launch_bounds__(kAttendThreads) void attend_stream_kernel(AttendPar
   using S = Stream<DT, LPR, NQ, KV, QDT>;
   constexpr int R = S::R, NB = S::NB, D = S::D, VEC = S::VEC, NWAVE = S::NWAVE;
   __shared__ int s_off[kMaxLists + 1];
+  __shared__ float s_fo[NWAVE * NQ * D];
+  __shared__ float s_fm[NWAVE * NQ], s_fl[NWAVE * NQ];
 
   const int H = p.num_kv_heads;
   const int nl = p.num_segments * H;
@@ -868,25 +872,39 @@ __global__ __launch_bounds__(kAttendThreads) void attend_stream_kernel(AttendPar
 
   typename S::State st;
   typename S::Query qr;
-  // This wave's partial of list L's piece; lanes 0..LPR-1 hold the merged state.
+  // The workgroup's partial of list L's piece: each wave merges its slots
+  // (lanes 0..LPR-1 hold the result), then the waves merge through LDS.
   auto flush = [&](int L) {
     S::merge_wave(st);
-    const int64_t item = ((int64_t)w + L) * NWAVE + wave;
     if (lane < LPR) {
-      float* po = p.part_o + item * kQG * D + cc * VEC;
 #pragma unroll
       for (int g = 0; g < NQ; ++g) {
 #pragma unroll
-        for (int e = 0; e < VEC; e += 4)
-          *reinterpret_cast<float4*>(po + g * D + e) =
-              make_float4(st.o[g][e], st.o[g][e + 1], st.o[g][e + 2], st.o[g][e + 3]);
-      }
-      if (lane == 0) {
-        float* pml = p.part_ml + item * kQG * 2;
-#pragma unroll
-        for (int g = 0; g < NQ; ++g) { pml[2 * g] = st.m[g]; pml[2 * g + 1] = st.l[g]; }
+        for (int e = 0; e < VEC; ++e) s_fo[(wave * NQ + g) * D + cc * VEC + e] = st.o[g][e];
+        if (lane == 0) { s_fm[wave * NQ + g] = st.m[g]; s_fl[wave * NQ + g] = st.l[g]; }
       }
     }
+    lds_barrier();
+    const int64_t item = (int64_t)w + L;
+    float* po = p.part_o + item * kQG * D;
+    float* pml = p.part_ml + item * kQG * 2;
+    for (int e = t; e < NQ * D; e += kAttendThreads) {
+      const int g = e / D, d = e - g * D;
+      float mm = -INFINITY;
+#pragma unroll
+      for (int v = 0; v < NWAVE; ++v) mm = fmaxf(mm, s_fm[v * NQ + g]);
+      float acc = 0.f, ll = 0.f;
+#pragma unroll
+      for (int v = 0; v < NWAVE; ++v) {
+        const float ms = s_fm[v * NQ + g];
+        const float wt = (ms == -INFINITY) ? 0.f : exp2f(ms - mm);
+        acc = fmaf(s_fo[(v * NQ + g) * D + d], wt, acc);
+        ll = fmaf(s_fl[v * NQ + g], wt, ll);
+      }
+      po[g * D + d] = acc;
+      if (d == 0) { pml[2 * g] = mm; pml[2 * g + 1] = ll; }
+    }
+    lds_barrier();  // every wave has read the staging before the next flush
   };
   auto is_uniform = [&](int L) { return p.uniform != nullptr && ld_const(p.uniform + L) != 0; };
   // List of chunk g, from a pointer that only moves forward.
@@ -1051,7 +1069,7 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
 constexpr int kListBatch = 256;  // partials whose weights are staged per round
 
 __global__ __launch_bounds__(256) void combine_lists_kernel(AttendParams p) {
-  constexpr int NWS = kAttendThreads / kWave;  // partials per piece (one per wave)
+  constexpr int NWS = 1;                        // partials per piece (one per workgroup)
   constexpr int MQ = kLogitsMaxQ;              // the ranges form carries at most 4 query rows
   constexpr int EPT = MQ * 512 / 256;          // output elements per thread (head_dim <= 512)
   __shared__ int s_off[kMaxLists + 1];
@@ -1273,8 +1291,8 @@ static hipError_t launch_stream(const AttendParams& p, hipStream_t s) {
 // ring).  At most 4 query rows per kv head and whole 512-token blocks; keys
 // and values (no logits) also need a block of whole chunks.  The split form
 // needs one segment and a unified list (its list fits LDS); the ranges form
-// takes any lists, with few enough workgroups that its (w + L) * waves
-// partial slots fit the per-item workspace.
+// takes any lists, with few enough workgroups that its w + L partial slots
+// fit the per-item workspace.
 void attend_stream_plan(AttendParams& p) {
   p.stream = kStreamNone;
   p.splits = 0;
@@ -1293,7 +1311,7 @@ void attend_stream_plan(AttendParams& p) {
   // Ranges-form workgroups: one per CU, two where the kernel fits two (four
   // query rows with logits: C3 layer 350.5 -> 345.5 us).
   const int64_t cap = (p.logits && attend_nq_bucket(p.sq * p.group) == 4) ? 512 : 256;
-  const int64_t room = attend_max_items(p) / (kAttendThreads / kWave) - nl;
+  const int64_t room = attend_max_items(p) - nl;
   const int64_t g = room < cap ? room : cap;
   if (g >= 1 && !p.keep) {
     p.stream = kStreamRanges;

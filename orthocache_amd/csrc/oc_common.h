@@ -156,6 +156,14 @@ __device__ __forceinline__ void st16_nt(void* p, float4 v) {
 // 138.8 -> 137.7 us; the decode partials measured slower this way).
 __device__ __forceinline__ void st4_nt(float* p, float v) { __builtin_nontemporal_store(v, p); }
 
+// Workgroup barrier that orders LDS accesses only: s_waitcnt lgkmcnt(0) +
+// s_barrier, without waiting for the vector memory loads in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // -------------------------------------------------------------- reductions
 // jnp.max semantics: NaN in either operand propagates.
 __device__ __forceinline__ float nanmax(float a, float b) { return (a > b || a != a) ? a : b; }

@@ -409,25 +409,25 @@ def test_streaming_lazy_rescale_rising_logits(dev, form):
 
 
 def test_ranges_combine_many_partials(dev):
-    """One list far longer than the others: with four query rows the ranges
-    form cuts all chunks into ~400 ranges, so the long list is merged from
-    640 partials -- more than one batch of staged weights in the per-list
-    combine.  Against the key-reading attention (a different partition) and
-    the oracle."""
+    """One list far longer than the other: with four query rows the ranges
+    form cuts the 4808 chunks into 512 ranges of 10, so the long list is
+    merged from 480 partials (one per workgroup piece) -- more than one batch
+    of staged weights in the per-list combine.  Against the key-reading
+    attention (a different partition) and the oracle."""
     from orthocache_amd import _ops
 
-    hkv, hq, d = 2, 8, 128
-    seg_blocks = [200, 2]
+    hkv, hq, d = 1, 4, 128
+    seg_blocks = [600, 2]
     nb = sum(seg_blocks)
     gen = torch.Generator(device=dev)
     gen.manual_seed(51)
     k = torch.randn(nb * 512, hkv, d, generator=gen, device=dev).to(torch.bfloat16)
     v = torch.randn(nb * 512, hkv, d, generator=gen, device=dev).to(torch.bfloat16)
     q = torch.randn(len(seg_blocks), 1, hq, d, generator=gen, device=dev).to(torch.bfloat16)
-    cu = torch.tensor([0, 200, 202], dtype=torch.int32, device=dev)
+    cu = torch.tensor([0, 600, 602], dtype=torch.int32, device=dev)
     m = np.zeros(nb, bool)
-    m[:200] = True
-    m[201] = True
+    m[:600] = True
+    m[601] = True
     c = _ops.mask_compact(num_blocks=nb, num_kv_heads=hkv, device=dev, mask_in=torch.from_numpy(m).to(dev),
                           cu_blocks=cu, num_segments=2)
     sc = _ops.score(k, q, cu_blocks=cu, num_segments=2, want_logits=True)
@@ -437,5 +437,5 @@ def test_ranges_combine_many_partials(dev):
     torch.cuda.synchronize()
     close(np32(out_lg), np32(out_k), 1e-5)
     qn, kn, vn = np32(q), np32(k), np32(v)
-    close(np32(out_lg)[0], O.attention_active_blocks(qn[0], kn[:200 * 512], vn[:200 * 512], range(200)), 2e-3)
-    close(np32(out_lg)[1], O.attention_active_blocks(qn[1], kn[200 * 512:], vn[200 * 512:], [1]), 2e-3)
+    close(np32(out_lg)[0], O.attention_active_blocks(qn[0], kn[:600 * 512], vn[:600 * 512], range(600)), 2e-3)
+    close(np32(out_lg)[1], O.attention_active_blocks(qn[1], kn[600 * 512:], vn[600 * 512:], [1]), 2e-3)
