@@ -153,7 +153,8 @@ __device__ __forceinline__ void st16_nt(void* p, float4 v) {
 }
 
 // 4-byte form, for the prefill kernel's transposed split partials (C4 chunk
-// 138.8 -> 137.7 us; the decode partials measured slower this way).
+// 139.2 -> 138.7 us in a same-box A/B; the decode partials measured slower
+// this way).
 __device__ __forceinline__ void st4_nt(float* p, float v) { __builtin_nontemporal_store(v, p); }
 
 // Workgroup barrier that orders LDS accesses only: s_waitcnt lgkmcnt(0) +
