@@ -73,62 +73,94 @@ def event_time_us(fn, reps, torch):
     return start.elapsed_time(stop) * 1000.0 / reps
 
 
-def cpu_baseline(wl, tau, zmax, budget_s):
-    """Time oracle/oc_port.c (the reference algorithm in C/OpenMP) on this host."""
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.machine()
+
+
+def _host_bf16(t):
+    """A bf16 device tensor as a host uint16 array of its bit patterns."""
+    import numpy as np
+    import torch
+
+    return t.view(dtype=torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _time_host(step, budget_s, min_reps=20, max_reps=200):
+    """Median wall time of step() over at least min_reps runs after one
+    untimed run (the reference's bench() convention: median after warmup,
+    benchmarks/phase_d_indirect_dma.py:39-47); as many more runs as fit in
+    budget_s, up to max_reps.  Returns (median_s, reps, last result)."""
+    t0 = time.perf_counter()
+    res = step()
+    est = time.perf_counter() - t0
+    reps = max(min_reps, min(max_reps, int(budget_s / max(est, 1e-6))))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        res = step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], reps, res
+
+
+def _baseline(value_us, reps, sample):
+    from oracle import native as ON
+
+    return {"value": round(value_us, 1), "unit": "us", "cores": int(ON.port().oc_port_threads()), "kind": "port",
+            "sample": f"{sample}; median of {reps} after one warmup run; oracle/oc_port.c (the reference "
+                      f"algorithm in C/OpenMP: full 9-stage FWHT, band sums, bound, mask, stable partition, "
+                      f"fp32 online-softmax loop), {_cpu_model()}"}
+
+
+def cpu_baseline(wl, tau, zmax, budget_s, gpu_mask=None):
+    """Time oracle/oc_port.c (the reference algorithm in C/OpenMP) on this
+    host over the full C2 layer; the port's mask is compared with the GPU's."""
     import numpy as np
 
     from oracle import native as ON
     from oracle import oc_oracle as O
 
     ON.port()
-    k = wl.k.view(dtype=__import__("torch").int16).cpu().numpy().view(np.uint16)
-    v = wl.v.view(dtype=__import__("torch").int16).cpu().numpy().view(np.uint16)
+    k, v = _host_bf16(wl.k), _host_bf16(wl.v)
     q = wl.q.float().cpu().numpy()
-    hkv = k.shape[1]
-    qf = O.fold_gqa(q, hkv)
+    qf = O.fold_gqa(q, k.shape[1])
     nb = k.shape[0] // 512
 
-    def layer(nblk):
-        kk = k[: nblk * 512]
-        t0 = time.perf_counter()
-        tm, z = ON.port_score(kk, qf)
+    def layer():
+        tm, z = ON.port_score(k, qf)
         mask, idx, n = ON.port_compact(tm, z, tau, zmax)
-        ON.port_attend(q, k[: nblk * 512], v[: nblk * 512], idx, n)
-        return time.perf_counter() - t0, n
+        ON.port_attend(q, k, v, idx, n)
+        return mask, n
 
-    # Calibrate on a small sample, then run the full layer if it fits the budget.
-    t_small, _ = layer(8)
-    est_full = t_small * nb / 8
-    reps = max(1, min(5, int(budget_s / max(est_full, 1e-3))))
-    if est_full * reps <= budget_s * 1.5:
-        times = []
-        n = 0
-        for _ in range(reps):
-            t, n = layer(nb)
-            times.append(t)
-        times.sort()
-        value = times[len(times) // 2] * 1e6
-        sample = f"full C2 layer ({nb} blocks, num_active={n}), median of {reps}"
-    else:
-        nblk = max(8, int(budget_s / 3 / max(t_small / 8, 1e-6)))
-        nblk = min(nb, nblk)
-        times = [layer(nblk)[0] for _ in range(3)]
-        times.sort()
-        value = times[1] * 1e6 * nb / nblk
-        sample = f"{nblk} of {nb} blocks, median of 3, scaled by {nb}/{nblk}"
-    import platform
+    t_one = time.perf_counter()
+    layer()
+    t_one = time.perf_counter() - t_one
+    if t_one * 20 <= 3 * budget_s:
+        med, reps, (mask, n) = _time_host(layer, budget_s)
+        sample = f"full C2 layer ({nb} blocks), num_active={n}"
+        if gpu_mask is not None:
+            sample += ", mask " + ("equal to" if np.array_equal(mask, gpu_mask) else "DIFFERENT from") + " the GPU's"
+        return _baseline(med * 1e6, reps, sample)
+    # A slow host: time the first blocks and scale to the layer.
+    nblk = max(8, min(nb, int(nb * budget_s / (20 * t_one))))
+    kk, vv = k[: nblk * 512], v[: nblk * 512]
 
-    cpu_model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    return {"value": round(value, 1), "unit": "us", "cores": int(ON.port().oc_port_threads()), "kind": "port",
-            "sample": sample + f"; oracle/oc_port.c (full 9-stage FWHT, fp32), {cpu_model or platform.machine()}"}
+    def part():
+        tm, z = ON.port_score(kk, qf)
+        _, idx, n = ON.port_compact(tm, z, tau, zmax)
+        ON.port_attend(q, kk, vv, idx, n)
+
+    med, reps, _ = _time_host(part, budget_s)
+    return _baseline(med * 1e6 * nb / nblk, reps, f"first {nblk} of {nb} C2 blocks, scaled by {nb}/{nblk}")
 
 
 def main():
@@ -225,10 +257,15 @@ def main():
     else:
         attend_bytes = 2 * kv_retained + q_bytes + out_bytes
     moved_bytes = score_bytes + compact_bytes + attend_bytes
-    score_gbs = score_bytes / (score_us * 1e-6) / 1e9
+    # The roofline counts the scoring kernel's algorithmic bytes of the
+    # metric's model (keys once, queries, 8 B of scores per tile); the logits
+    # it also stores for the attention are listed on their own.
+    score_model_bytes = s * hkv * d * esz + q_bytes + nb * hkv * 8
+    score_gbs = score_model_bytes / (score_us * 1e-6) / 1e9
     # score_kernel<key dtype, lanes per row, query dtype, logit query slots>
     kernel = f"score_kernel<bf16, 32, bf16, {nqp if logits else 0}>"
     traffic = None
+    traffic_src = None
     tpath = os.path.join(ROOT, "profiles", "score_kernel_c2_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
@@ -236,6 +273,9 @@ def main():
         # Counters measured for this very kernel variant only.
         if tj.get("kernel") == kernel:
             traffic = tj.get("bytes_per_launch")
+            traffic_src = ("profiles/score_kernel_c2_traffic.json: rocprofv3 FETCH_SIZE + WRITE_SIZE of this "
+                           "kernel variant at this workload, scaled by a plain copy kernel's counters; "
+                           "not measured by this run")
 
     result = {
         "metric": METRIC,
@@ -264,11 +304,15 @@ def main():
                        "attend_and_combine": round(attend_us, 2)},
         "roofline": {"bound": "hbm", "kernel": kernel, "achieved": round(score_gbs, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(score_gbs / PEAK_HBM_GBS, 4),
-                     "traffic": traffic},
+                     "traffic": traffic, "traffic_source": traffic_src,
+                     "algorithmic_bytes": score_model_bytes, "logits_store_bytes": logit_bytes,
+                     "kernel_us": round(score_us, 2)},
     }
     if not args.no_cpu:
         try:
-            result["cpu_baseline"] = cpu_baseline(wl, tau, zmax, args.cpu_budget)
+            gm = _ops.mask_compact(num_blocks=nb, num_kv_heads=hkv, device=dev, tau_max=layer.tau_max,
+                                   zeta=layer.zeta, tau=tau, zeta_max=zmax, want_mask=True, want_indices=False)
+            result["cpu_baseline"] = cpu_baseline(wl, tau, zmax, args.cpu_budget, gpu_mask=gm.mask.cpu().numpy())
         except Exception as e:  # the GPU result stands without it
             result["cpu_baseline"] = {"error": f"{type(e).__name__}: {e}"}
     print(json.dumps(result), flush=True)
@@ -326,7 +370,34 @@ def run_c4(args, torch, dev):
                      "achieved": round(tflops, 1), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(tflops / peak, 4), "traffic": None},
     }
+    if not args.no_cpu:
+        try:
+            result["cpu_baseline"] = cpu_baseline_c4(wl, tau, zmax, args.cpu_budget, num_active)
+        except Exception as e:
+            result["cpu_baseline"] = {"error": f"{type(e).__name__}: {e}"}
     print(json.dumps(result), flush=True)
+
+
+def cpu_baseline_c4(wl, tau, zmax, budget_s, gpu_active):
+    """The C/OpenMP port over the whole C4 chunk: scores with the bound of all
+    512 queries, mask + compaction, attention of every query row."""
+    from oracle import native as ON
+    from oracle import oc_oracle as O
+
+    k, v = _host_bf16(wl.k), _host_bf16(wl.v)
+    q = wl.q.float().cpu().numpy()
+    qf = O.fold_gqa(q, k.shape[1])
+
+    def step():
+        tm, z = ON.port_score(k, qf)
+        _, idx, n = ON.port_compact(tm, z, tau, zmax)
+        ON.port_attend(q, k, v, idx, n)
+        return n
+
+    # About 2 s per chunk on 16 EPYC threads: at least 10 runs, not 20.
+    med, reps, n = _time_host(step, budget_s, min_reps=10)
+    return _baseline(med * 1e6, reps, f"full C4 chunk (512 queries x 256 blocks), num_active={n} "
+                                      f"(GPU {gpu_active})")
 
 
 def _line(metric, us, args, config, extra):
@@ -421,14 +492,59 @@ def run_c3(args, torch, dev):
     attend_bytes = kept * 512 * hkv * d * 2 * 2 + q_bytes + wl.q.numel() * 2
     total = score_bytes + attend_bytes
     gbs = total / (us * 1e-6) / 1e9
+    score_gbs = score_bytes / (kus["score"] * 1e-6) / 1e9
+    nq = wl.q.shape[-3] * (hq // hkv)
+    extra = {"algorithmic_bytes": total, "layer_gbps": round(gbs, 1),
+             "layer_frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
+             "kernels_us": {k: round(v, 2) for k, v in kus.items()},
+             "roofline": {"bound": "hbm",
+                          "kernel": f"score_kernel<bf16, 16, bf16, {_ops.logits_nq_pad(nq)}> (segments)",
+                          "achieved": round(score_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                          "frac": round(score_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                          "algorithmic_bytes": score_bytes, "kernel_us": round(kus["score"], 2)}}
+    if not args.no_cpu:
+        try:
+            extra["cpu_baseline"] = cpu_baseline_segments(wl, tau_t.cpu().numpy(), zmax_t.cpu().numpy(),
+                                                          args.cpu_budget, attend=True, gpu_active=kept)
+        except Exception as e:
+            extra["cpu_baseline"] = {"error": f"{type(e).__name__}: {e}"}
     print(json.dumps(_line("us per batched decode layer score+compact+attend, C3 ragged batch 32",
                            us, args,
                            {"workload": wl.name, "batch": nseg, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
                             "tokens": s, "blocks": s // 512, "retained_blocks": kept,
-                            "evict_range": [0.30, 0.95]},
-                           {"algorithmic_bytes": total, "layer_gbps": round(gbs, 1),
-                            "layer_frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
-                            "kernels_us": {k: round(v, 2) for k, v in kus.items()}})), flush=True)
+                            "evict_range": [0.30, 0.95]}, extra)), flush=True)
+
+
+def cpu_baseline_segments(wl, taus, zmaxs, budget_s, attend, gpu_active):
+    """The C/OpenMP port over every segment of a ragged batch (C3) or layer of
+    a sweep (C5): per segment its scores, mask + compaction and (C3) attention,
+    as the reference runs one sequence per call."""
+    import numpy as np
+
+    from oracle import native as ON
+    from oracle import oc_oracle as O
+
+    cu = (wl.cu_seqlens.cpu().numpy() // 512).astype(np.int64)
+    k = _host_bf16(wl.k)
+    v = _host_bf16(wl.v) if attend else None
+    q = wl.q.float().cpu().numpy()
+    hkv = k.shape[1]
+    segs = [(int(cu[i]) * 512, int(cu[i + 1]) * 512, O.fold_gqa(q[i], hkv)) for i in range(len(cu) - 1)]
+
+    def step():
+        kept = 0
+        for i, (lo, hi, qf) in enumerate(segs):
+            tm, z = ON.port_score(k[lo:hi], qf)
+            _, idx, n = ON.port_compact(tm, z, float(taus[i]), float(zmaxs[i]))
+            kept += n
+            if attend:
+                ON.port_attend(q[i], k[lo:hi], v[lo:hi], idx, n)
+        return kept
+
+    med, reps, kept = _time_host(step, budget_s)
+    what = "attention" if attend else "no attention"
+    return _baseline(med * 1e6, reps, f"all {len(segs)} segments, one port call per segment ({what}), "
+                                      f"{kept} blocks kept (GPU {gpu_active})")
 
 
 def run_c5(args, torch, dev):
@@ -454,14 +570,27 @@ def run_c5(args, torch, dev):
         sweep()
     torch.cuda.synchronize()
     us = event_time_us(sweep, args.steps, torch)
+    kept = int(sweep()[2].sum().item())
+    score_us = event_time_us(lambda: varlen.score_varlen(wl.q, wl.k, wl.cu_seqlens), args.kernel_reps, torch)
     s, hkv, d = wl.k.shape
     score_bytes = s * hkv * d * 2 + wl.q.numel() * 2 + (s // 512) * hkv * 8
     gbs = score_bytes / (us * 1e-6) / 1e9
+    score_gbs = score_bytes / (score_us * 1e-6) / 1e9
+    extra = {"algorithmic_bytes": score_bytes, "sweep_gbps": round(gbs, 1),
+             "sweep_frac_of_peak": round(gbs / PEAK_HBM_GBS, 4), "retained_blocks": kept,
+             "roofline": {"bound": "hbm", "kernel": "score_kernel<bf16, 32, bf16, 0> (60 layers as segments)",
+                          "achieved": round(score_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                          "frac": round(score_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                          "algorithmic_bytes": score_bytes, "kernel_us": round(score_us, 2)}}
+    if not args.no_cpu:
+        try:
+            extra["cpu_baseline"] = cpu_baseline_segments(wl, tau_t.cpu().numpy(), zmax_t.cpu().numpy(),
+                                                          args.cpu_budget, attend=False, gpu_active=kept)
+        except Exception as e:
+            extra["cpu_baseline"] = {"error": f"{type(e).__name__}: {e}"}
     print(json.dumps(_line("us per 60-layer scoring sweep (score + mask + compaction), C5", us, args,
                            {"workload": wl.name, "layers": nl, "kv_heads": hkv, "head_dim": d, "tokens": s,
-                            "blocks": s // 512, "evict": 0.9},
-                           {"algorithmic_bytes": score_bytes, "sweep_gbps": round(gbs, 1),
-                            "sweep_frac_of_peak": round(gbs / PEAK_HBM_GBS, 4)})), flush=True)
+                            "blocks": s // 512, "evict": 0.9}, extra)), flush=True)
 
 
 if __name__ == "__main__":

@@ -20,6 +20,8 @@
  *    workspaces are caller-owned.  Counts such as num_active stay on device.
  *  - Return 0 on success or a negative OC_ERR_* code; oc_last_error() gives
  *    a message (thread-local).  Entry points are stateless and reentrant.
+ *  - Workspaces must be 256-byte aligned (hipMalloc and torch allocations
+ *    are); an unaligned one is rejected with OC_ERR_INVALID_ARGUMENT.
  *  - Paged caches: the argument structs of scoring, attention and the layer
  *    take `pages`, an int32 device array (total_blocks): the block with
  *    flattened index j (segment offsets included) lives in physical page
@@ -208,7 +210,14 @@ int oc_mask_compact(const oc_compact_args* a, void* stream);
  * (stream_compact's gather, src/orthocache/compaction.py:86-98;
  * stream_decompact, :103-154).  scatter = 0: dst[i] = src[indices[i]] for
  * i < *num_active, zero otherwise; scatter = 1: dst[indices[i]] = src[i] for
- * i < *num_active, zero otherwise.  block_bytes must be a multiple of 16. */
+ * i < *num_active, zero for every block no such i names.  block_bytes must
+ * be a multiple of 16.  Every one of the num_blocks destination blocks is
+ * written exactly once, whatever the list holds: entries in [-num_blocks, 0)
+ * count from the end (NumPy indexing); other entries outside [0, num_blocks)
+ * are clamped into it by the gather and dropped by the scatter (JAX's
+ * gather / scatter rules); if several positions i < *num_active name one
+ * block, the scatter takes the last of them; *num_active is clamped into
+ * [0, num_blocks]. */
 int oc_copy_blocks(const void* src, void* dst, const int32_t* indices, const int32_t* num_active,
                    int32_t num_blocks, int64_t block_bytes, int32_t scatter, void* stream);
 

@@ -26,11 +26,24 @@ Pinning (what checks each function independently of its own formula):
   and the Cauchy-Schwarz invariant bound >= max_i q.k_i / sqrt(d).
 * ``mask_from_scores`` / masks: the reference tests' threshold-mask known
   answer, NaN semantics, and the two-gate test of
-  ``tests/test_spectral_bands.py:177-213`` regenerated from its seed.
+  ``tests/test_spectral_bands.py:177-213`` regenerated from its seed (exact
+  mask, and a variant with the reference's Walsh-coherent block that the zeta
+  gate keeps).
+* ``query_aware_mask`` / ``multiband_mask``: literal masks on keys built from
+  natural-order Walsh rows 1 and 256 plus a mean, whose band energies, zeta,
+  kbar and E_AC follow from the construction (orthogonality of the rows); a
+  sequency-ordered transform fails them.
+* ``auto_tau`` / ``auto_tau_from_max_bounds``: the known answer mean - population
+  std of [1, 2, 3, 4] = 2.5 - sqrt(1.25) (a sample std fails it), and the
+  Walsh construction's bounds in closed form.
 * ``stream_compact_indices``: the compaction known answers of
   ``tests/test_alltoallv.py:60-67``, ``tests/test_distributed.py:57-64`` and
   ``tests/test_adaptive_attention.py:60-67`` plus brute-force stable
-  partition.
+  partition; an unstable (Hoare) partition fails the first known answer.
+* ``stream_decompact``: the compact -> decompact round trip on a permutation;
+  lists that are not one follow JAX's scatter rules (negative entries count
+  from the end, out-of-bounds entries are dropped) with positions applied in
+  order.
 * ``attention_*``: float64 closed-form softmax over the retained tokens, and
   the reference's own C++ CPU attention (``notebooks/phase_d_kaggle.py``
   custom call) when ``oracle/_ref`` has been built from the reference.
@@ -234,10 +247,21 @@ def stream_compact(keys, values, block_mask, block_size=BLOCK):
 
 
 def stream_decompact(compact, active_indices, num_active, num_blocks):
-    """``compaction.py:103-154``: out[active[i]] = compact[i] if i < n else 0."""
+    """``compaction.py:103-154``: out[active[i]] = compact[i] if i < n else 0.
+
+    The reference scatters with ``output.at[active_indices].set(...)``: a
+    negative entry counts from the end (NumPy indexing), an entry still out
+    of bounds is dropped (JAX scatter), and for repeated entries the order is
+    left to the implementation; here positions are applied in order, so the
+    last position i < n naming a block wins.
+    """
     out = np.zeros((num_blocks,) + compact.shape[1:], dtype=compact.dtype)
-    for i, j in enumerate(np.asarray(active_indices)[:num_blocks]):
-        if i < num_active:
+    n = max(0, min(int(num_active), num_blocks))
+    for i, j in enumerate(np.asarray(active_indices)[:n]):
+        j = int(j)
+        if -num_blocks <= j < 0:
+            j += num_blocks
+        if 0 <= j < num_blocks:
             out[j] = compact[i]
     return out
 
@@ -379,10 +403,18 @@ def next_bucket(n, buckets=(1, 2, 4, 8, 16, 32, 64, 128, 256, 512)):
     return n
 
 
-def auto_tau(q, keys, block_size=BLOCK, dtype=np.float64):
-    """mean - std of the per-(block, head) max bound: ``pipeline.py:168-176``."""
-    mb = nanmax_axis0(query_aware_bounds(q, keys, block_size, dtype))
+def auto_tau_from_max_bounds(max_bounds):
+    """mean - std over every (block, head) entry of the max bound:
+    ``pipeline.py:174-176``.  ``jnp.std`` defaults to ddof=0, the population
+    standard deviation, as ``np.std`` does."""
+    mb = np.asarray(max_bounds, dtype=np.float64)
     return float(np.mean(mb) - np.std(mb))
+
+
+def auto_tau(q, keys, block_size=BLOCK, dtype=np.float64):
+    """mean - std of the per-(block, head) max bound: ``pipeline.py:168-176``
+    (the max over queries is ``:173``)."""
+    return auto_tau_from_max_bounds(nanmax_axis0(query_aware_bounds(q, keys, block_size, dtype)))
 
 
 # --------------------------------------------------------------------------

@@ -54,7 +54,8 @@ def orthocache_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.
                       out_dtype=torch.bfloat16)
     n = int(c.num_active[0].item())
     if n == 0:
-        return out, {"num_active": 0, "eviction_rate": 1.0, "path": "zero"}
+        # adaptive_attention.py:164-167 returns zeros_like(q) (q's dtype)
+        return torch.zeros_like(q), {"num_active": 0, "eviction_rate": 1.0, "path": "zero"}
     return out, {"num_active": n, "num_blocks": nb, "eviction_rate": 1.0 - n / nb, "path": _path(seq_k)}
 
 
@@ -82,7 +83,7 @@ def orthocache_attention_batched(q: torch.Tensor, k_cache: torch.Tensor, v_cache
                       cu_blocks=cu, num_segments=b)
     n = int(c.num_active[0].item())
     if n == 0:
-        return out, {"num_active": 0, "eviction_rate": 1.0, "path": "zero"}
+        return torch.zeros_like(q), {"num_active": 0, "eviction_rate": 1.0, "path": "zero"}
     return out, {"num_active": n, "num_blocks": nb, "eviction_rate": 1.0 - n / nb, "batch_size": b,
                  "path": _path(seq_k, batched=True)}
 

@@ -46,7 +46,12 @@ def stream_decompact(compact_output: torch.Tensor, active_indices: torch.Tensor,
     """Scatter compacted blocks back: ``compaction.py:103-154``.
 
     out[active_indices[i]] = compact_output[i] for i < num_active; every other
-    block is zero.  active_indices must be the permutation from stream_compact.
+    block is zero.  With the permutation from stream_compact that is the
+    reference's result.  Other lists are safe: entries outside
+    [0, num_blocks_original) are dropped (JAX drops out-of-bounds scatter
+    updates; negative entries count from the end first), and when several
+    positions name one block the last of them wins (a JAX scatter leaves
+    that order to the implementation).
     """
     require_gpu(compact_output, active_indices)
     nb = num_blocks_original

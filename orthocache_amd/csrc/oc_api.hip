@@ -28,6 +28,8 @@ int hip_check(hipError_t e, const char* what) {
 bool valid_dtype(int dt) { return dt == OC_F32 || dt == OC_BF16 || dt == OC_F16; }
 int esize(int dt) { return dt == OC_F32 ? 4 : 2; }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+// Workspaces are carved at 256-byte offsets and read with 16-byte vector loads.
+bool aligned256(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 255u) == 0; }
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
 int check_kv(const char* name, const void* p, int dt, int64_t tok_stride, int64_t head_stride, int head_dim) {
@@ -268,15 +270,16 @@ int make_attend_params(const oc_attend_args* a, oc::AttendParams& p) {
   return OC_OK;
 }
 
-// Partial-result bytes: [o | (m, l)].
+// Partial-result bytes: [o | (m, l)], for the partials the launch of these
+// parameters writes (decode: one (kQG x D) + (kQG x 2) pair per slot).
 size_t attend_part_o_bytes(const oc::AttendParams& p) {
   if (p.prefill) return align256((size_t)oc::prefill_partial_floats(p) * sizeof(float));
-  return align256((size_t)oc::attend_max_items(p) * oc::kQG * p.head_dim * sizeof(float));
+  return align256((size_t)oc::attend_partial_slots(p) * oc::kQG * p.head_dim * sizeof(float));
 }
 
 size_t attend_part_ml_bytes(const oc::AttendParams& p) {
   if (p.prefill) return align256((size_t)oc::prefill_partial_floats(p) / p.head_dim * 2 * sizeof(float));
-  return align256((size_t)oc::attend_max_items(p) * oc::kQG * 2 * sizeof(float));
+  return align256((size_t)oc::attend_partial_slots(p) * oc::kQG * 2 * sizeof(float));
 }
 
 size_t attend_ws(const oc::AttendParams& p) { return attend_part_o_bytes(p) + attend_part_ml_bytes(p); }
@@ -315,6 +318,7 @@ int oc_attend(const oc_attend_args* a, void* workspace, size_t workspace_bytes, 
   const size_t need = attend_ws(p);
   if (need && (!workspace || workspace_bytes < need))
     return fail(OC_ERR_WORKSPACE, "workspace %zu bytes < %zu needed", workspace_bytes, need);
+  if (need && !aligned256(workspace)) return fail(OC_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
   attend_bind_ws(p, workspace);
   return hip_check(oc::launch_attend(p, (hipStream_t)stream), "oc_attend");
 }
@@ -385,16 +389,31 @@ oc_attend_args layer_attend_args(const oc_layer_args* a) {
   return t;
 }
 
+// The layer's attention parameters, with the scoring-pass logits and the
+// keep flags marked present exactly when the layer will pass them: the
+// attention's form, and with it the partial count and the workspace, depends
+// on both.  The markers are never dereferenced; decode_layer_impl replaces
+// them with the workspace addresses before launching.
+int layer_attend_params(const oc_layer_args* a, bool logits, oc::AttendParams& p) {
+  oc_attend_args t = layer_attend_args(a);
+  const int rc = make_attend_params(&t, p);
+  if (rc) return rc;
+  static const float marker = 0.f;
+  p.logits = logits ? &marker : nullptr;
+  p.keep = layer_uses_keep(a) ? reinterpret_cast<const uint8_t*>(&marker) : nullptr;
+  return OC_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
 size_t oc_decode_layer_workspace_size(const oc_layer_args* a) {
   if (!a) return 0;
-  oc_attend_args t = layer_attend_args(a);
+  const bool logits = layer_uses_logits(a);
   oc::AttendParams p;
-  if (make_attend_params(&t, p)) return 0;
-  return layer_ws_layout(a, attend_ws(p), layer_uses_logits(a)).total;
+  if (layer_attend_params(a, logits, p)) return 0;
+  return layer_ws_layout(a, attend_ws(p), logits).total;
 }
 
 }  // extern "C"
@@ -406,9 +425,9 @@ namespace {
 int decode_layer_impl(const oc_layer_args* a, const oc_block_stats* st, void* workspace, size_t workspace_bytes,
                       void* stream, const char* name) {
   if (!a) return fail(OC_ERR_INVALID_ARGUMENT, "args is NULL");
-  oc_attend_args t = layer_attend_args(a);
+  const bool use_logits = !st && layer_uses_logits(a);
   oc::AttendParams ap;
-  int rc = make_attend_params(&t, ap);
+  int rc = layer_attend_params(a, use_logits, ap);
   if (rc) return rc;
   if (st) {
     if (!st->dc || !st->e_ac || !st->zeta) return fail(OC_ERR_INVALID_ARGUMENT, "%s: NULL block statistics", name);
@@ -426,10 +445,10 @@ int decode_layer_impl(const oc_layer_args* a, const oc_block_stats* st, void* wo
     return fail(OC_ERR_UNSUPPORTED, "decode layer takes at most 16 queries per kv head (sq * group)");
   const int nseg = a->cu_blocks ? a->num_segments : 1;
   if (a->cu_blocks && nseg > 4096) return fail(OC_ERR_UNSUPPORTED, "at most 4096 segments per call");
-  const bool use_logits = !st && layer_uses_logits(a);
   const LayerWs w = layer_ws_layout(a, attend_ws(ap), use_logits);
   if (w.total && (!workspace || workspace_bytes < w.total))
     return fail(OC_ERR_WORKSPACE, "workspace %zu bytes < %zu needed", workspace_bytes, w.total);
+  if (w.total && !aligned256(workspace)) return fail(OC_ERR_INVALID_ARGUMENT, "%s: workspace must be 256-byte aligned", name);
   char* ws = static_cast<char*>(workspace);
   float* tau_max = a->tau_max ? a->tau_max : reinterpret_cast<float*>(ws + w.tau);
   const float* zeta_in;
@@ -484,6 +503,7 @@ int decode_layer_impl(const oc_layer_args* a, const oc_block_stats* st, void* wo
     ap.list_out = idx;
     ap.count_out = cnt;
   } else {
+    ap.keep = nullptr;
     oc::CompactParams cp{};
     cp.tau_max = tau_max; cp.tau_parts = 1; cp.zeta = zeta_in;
     cp.tau_arr = a->tau_arr; cp.tau = a->tau; cp.zmax_arr = a->zeta_max_arr; cp.zeta_max = a->zeta_max;
@@ -511,9 +531,8 @@ int oc_decode_layer(const oc_layer_args* a, void* workspace, size_t workspace_by
 
 size_t oc_decode_layer_cached_workspace_size(const oc_layer_args* a) {
   if (!a) return 0;
-  oc_attend_args t = layer_attend_args(a);
   oc::AttendParams p;
-  if (make_attend_params(&t, p)) return 0;
+  if (layer_attend_params(a, false, p)) return 0;
   return layer_ws_layout(a, attend_ws(p), false).total;
 }
 

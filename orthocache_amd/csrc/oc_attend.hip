@@ -1319,6 +1319,21 @@ void attend_stream_plan(AttendParams& p) {
   }
 }
 
+// Partial slots the decode launch of these parameters writes (the workspace
+// holds this many (kQG x D) + (kQG x 2) partials).  The split form writes
+// item split * Hkv + h for split < splits; the ranges form writes w + L for
+// workgroup w < splits and list L < segments * Hkv; the per-item form writes
+// at most one per work item, bounded by attend_max_items.  The plan depends
+// on whether logits and keep flags are given, so callers size with those
+// fields set as they will be at launch.
+int64_t attend_partial_slots(const AttendParams& p_in) {
+  AttendParams p = p_in;
+  attend_stream_plan(p);
+  if (p.stream == kStreamSplit) return (int64_t)p.num_kv_heads * p.splits;
+  if (p.stream == kStreamRanges) return (int64_t)p.splits + (int64_t)p.num_segments * p.num_kv_heads;
+  return attend_max_items(p);
+}
+
 hipError_t launch_attend(const AttendParams& p_in, hipStream_t s) {
   if (p_in.prefill) return launch_prefill(p_in, s);
   AttendParams p = p_in;

@@ -27,19 +27,49 @@ __global__ __launch_bounds__(256) void compact_kernel(CompactParams p) {
   compact_segment(p, blockIdx.x, s_flag, kFlagBytes, s_act, kActCap, s_cnt);
 }
 
+// A list entry as NumPy-style indexing reads it: -nb <= i < 0 counts from
+// the end.  Entries still outside [0, nb) are returned as is.
+__device__ __forceinline__ int wrap_index(int i, int nb) { return (i < 0 && i >= -nb) ? i + nb : i; }
+
 // Block copy for the materialised compaction API (compaction.py:86-98,
-// :103-154).  gather: dst[i] = src[idx[i]] for i < n, zero for i >= n.
-// scatter: dst[idx[i]] = src[i] for i < n, zero for i >= n.  Blocks are
-// contiguous runs of block_bytes (layout (seq, heads, dim)).
+// :103-154).  Blocks are contiguous runs of block_bytes (layout (seq, heads,
+// dim)); workgroup row blockIdx.y owns destination block j, so every
+// destination block is written exactly once, whatever the list holds.
+//  gather:  dst[j] = src[idx[j]] for j < n, zero for j >= n.  An entry
+//           outside [0, nb) is clamped into it (JAX clamps gather indices).
+//  scatter: dst[j] = src[i] for the largest i < n with idx[i] == j, zero when
+//           no such i exists.  Entries outside [0, nb) are dropped (JAX drops
+//           out-of-bounds scatter updates).  For a permutation this is
+//           dst[idx[i]] = src[i] for i < n; for duplicate entries, whose
+//           order a JAX scatter leaves to the implementation, the last list
+//           position wins.
 __global__ __launch_bounds__(256) void copy_blocks_kernel(CopyParams p) {
-  const int i = blockIdx.y;
-  const int n = *p.num_active;
-  const int idx = p.indices[i];
-  const bool live = i < n;
-  const int64_t src_blk = p.scatter ? i : idx;
-  const int64_t dst_blk = p.scatter ? idx : i;
-  const uint4* s = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(p.src) + src_blk * p.block_bytes);
-  uint4* d = reinterpret_cast<uint4*>(reinterpret_cast<char*>(p.dst) + dst_blk * p.block_bytes);
+  __shared__ int s_owner[4];
+  const int j = blockIdx.y;
+  const int nb = p.num_blocks;
+  int n = *p.num_active;
+  n = n < 0 ? 0 : (n > nb ? nb : n);
+  int src_blk = -1;
+  if (!p.scatter) {
+    if (j < n) {
+      const int s = wrap_index(p.indices[j], nb);
+      src_blk = s < 0 ? 0 : (s >= nb ? nb - 1 : s);
+    }
+  } else {
+    // Each thread keeps its last matching position; positions rise with the
+    // loop, so the maxima over threads and waves give the last one overall.
+    int own = -1;
+    for (int i = threadIdx.x; i < n; i += blockDim.x)
+      if (wrap_index(p.indices[i], nb) == j) own = i;
+    for (int off = 32; off > 0; off >>= 1) own = max(own, __shfl_xor(own, off, 64));
+    if ((threadIdx.x & 63) == 0) s_owner[threadIdx.x >> 6] = own;
+    __syncthreads();
+    src_blk = max(max(s_owner[0], s_owner[1]), max(s_owner[2], s_owner[3]));
+  }
+  const bool live = src_blk >= 0;
+  const uint4* s = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(p.src) +
+                                                  (int64_t)(live ? src_blk : 0) * p.block_bytes);
+  uint4* d = reinterpret_cast<uint4*>(reinterpret_cast<char*>(p.dst) + (int64_t)j * p.block_bytes);
   const int64_t nvec = p.block_bytes / 16;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < nvec; e += (int64_t)gridDim.x * blockDim.x) {
     d[e] = live ? s[e] : make_uint4(0u, 0u, 0u, 0u);

@@ -236,6 +236,7 @@ bool attend_supported(int dt, int head_dim);
 int attend_nq_bucket(int nq_total);
 int attend_chunk(int dt, int head_dim, int nq_total);  // tokens per work item
 int64_t attend_max_items(const AttendParams& p);
+int64_t attend_partial_slots(const AttendParams& p);  // partials the decode launch writes
 hipError_t launch_attend(const AttendParams& p, hipStream_t s);
 
 // ---------------------------------------------------------- oc_prefill.hip

@@ -53,25 +53,46 @@ def make_queries(shape, d: int, *, seed: int, device, dtype=torch.bfloat16) -> t
     return (torch.randn(tuple(shape), generator=g, device=device, dtype=torch.float32) / math.sqrt(d)).to(dtype)
 
 
+def _f32(x: float) -> float:
+    return float(torch.tensor(x, dtype=torch.float32))
+
+
+def _between(lo: float, hi: float) -> float:
+    """An fp32 threshold t with lo < t <= hi for fp32 values lo < hi: their
+    midpoint rounded to fp32, or hi when no fp32 value lies strictly between."""
+    t = _f32((lo + hi) / 2.0)
+    return t if lo < t <= hi else hi
+
+
 def calibrate_unified(tau_max: torch.Tensor, zeta: torch.Tensor, evict: float, zeta_quantile: float = 0.95):
     """(tau, zeta_max) so that the unified two-gate mask keeps round(nb*(1-evict)) blocks.
 
-    zeta_max is the given quantile of zeta over (block, head); a block's
-    unified score is the max tau_max over the heads that pass the zeta gate;
-    tau is the K-th largest unified score (an fp32 value, so the fp32 compare
-    keeps exactly the top K when scores are distinct).  Host-synchronising;
-    done once, outside any timed region.
+    zeta_max lies at the given quantile of zeta over (block, head), halfway
+    between the two neighbouring fp32 values there; a block's unified score is
+    the max tau_max over the heads that pass the zeta gate; tau lies halfway
+    between the K-th and (K+1)-th largest unified scores, so the fp32 compare
+    keeps exactly the top K when those differ, and no score sits on the
+    threshold (a restatement that rounds a score differently in its last bits
+    keeps the same blocks).  Host-synchronising; done once, outside any timed
+    region.
     """
     nb = tau_max.shape[0]
-    zmax = float(torch.quantile(zeta.flatten().float(), zeta_quantile).item())
-    zmax = float(torch.tensor(zmax, dtype=torch.float32))
+    zs = torch.sort(zeta.flatten().float()).values
+    i = min(int(zeta_quantile * (zs.numel() - 1)), zs.numel() - 1)
+    j = i
+    while j + 1 < zs.numel() and float(zs[j + 1]) == float(zs[i]):
+        j += 1
+    zmax = float(zs[i]) if j + 1 >= zs.numel() else _between(float(zs[i]), float(zs[j + 1]))
     ok = zeta <= zmax
     u = torch.where(ok, tau_max, torch.full_like(tau_max, -math.inf)).amax(dim=-1)
     keep = int(round(nb * (1.0 - evict)))
     if keep <= 0:
         return math.inf, zmax
-    vals = torch.sort(u, descending=True).values
-    return float(vals[min(keep, nb) - 1].item()), zmax
+    vals = torch.sort(u, descending=True).values.tolist()
+    kth = vals[min(keep, nb) - 1]
+    if keep >= nb or vals[keep] == -math.inf or vals[keep] == kth:
+        return kth, zmax
+    return _between(vals[keep], kth), zmax
 
 
 def percentile(x: torch.Tensor, q: float) -> float:

@@ -171,3 +171,39 @@ class TestMaterialised:
         assert int(n) == 4 and np32(idx).tolist() == [0, 1, 2, 3]
         _, _, _, n = oc.stream_compact(k[:512], k[:512], torch.ones(1, 2, dtype=torch.bool, device=dev))
         assert int(n) == 1
+
+    @pytest.mark.parametrize("idx,n", [
+        ([3, 1, 3, 0, 5, 2], 4),         # block 3 named twice: the later position (2) wins
+        ([7, -1, 9, 2, -6, 0], 6),       # out of range (7, 9, -7..) dropped; -1 -> 5, -6 -> 0
+        ([1, 1, 1, 1, 1, 1], 6),         # every position names block 1: position 5 wins
+        ([4, 0, 2, 1, 3, 5], 9),         # num_active beyond the block count is clamped to 6
+        ([4, 0, 2, 1, 3, 5], -2),        # and below zero to 0: all zeros
+    ])
+    def test_decompact_arbitrary_lists(self, dev, idx, n):
+        """stream_decompact on lists that are not stream_compact's permutation:
+        every destination block is written once, out-of-range entries are
+        dropped, repeated entries take the last position (the oracle's
+        in-order scatter); the gather clamps its entries."""
+        import orthocache_amd as oc
+        from orthocache_amd import _ops
+
+        nb, h, d = 6, 2, 32
+        src = torch.randn(nb, 512, h, d, device=dev)
+        ind = torch.tensor(idx, dtype=torch.int32, device=dev)
+        out = oc.stream_decompact(src, ind, n, nb)
+        torch.cuda.synchronize()
+        ref = O.stream_decompact(np32(src), np.array(idx), n, nb)
+        np.testing.assert_array_equal(np32(out), ref)
+        # gather form: dst[i] = src[clamp(wrap(idx[i]))] for i < n
+        dst = torch.empty_like(src)
+        na = torch.tensor([n], dtype=torch.int32, device=dev)
+        _ops.copy_blocks(src.reshape(nb, -1), dst, ind, na, nb, scatter=False)
+        torch.cuda.synchronize()
+        nn = max(0, min(n, nb))
+        s = np32(src)
+        for i in range(nb):
+            if i < nn:
+                j = idx[i] + nb if -nb <= idx[i] < 0 else idx[i]
+                np.testing.assert_array_equal(np32(dst[i]), s[min(max(j, 0), nb - 1)])
+            else:
+                assert float(dst[i].abs().sum()) == 0.0

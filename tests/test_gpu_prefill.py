@@ -182,3 +182,46 @@ def test_c4_full_size_sampled_rows(dev):
     ref = O.attention_active_blocks(np32(q[rows]), np32(k), np32(v), act)
     close(np32(out[rows]), ref, 5e-3)
     assert torch.isfinite(out).all()
+
+
+def test_c4_prefill_layer_as_benched(dev):
+    """C4 as bench.py times it: PrefillLayer (scoring -> bounds of all 512
+    queries on the tiled kernel -> two-gate mask + compaction over the
+    64-query tile maxima -> MFMA attention) on workloads.c4 at full size
+    (131072 keys, 8 kv heads, d = 128, bf16), 75% evicted.  Tile maxima of
+    sampled blocks against the float64 oracle; mask, permutation and count
+    bit-exact against the oracle on the layer's own fp32 scores; sampled
+    query rows against the float64 oracle over the retained blocks."""
+    from orthocache_amd import _ops, workloads
+
+    wl = workloads.c4(dev)
+    sc = _ops.score(wl.k, wl.q)
+    tau, zmax = workloads.calibrate_unified(sc.tau_max.amax(dim=0), sc.zeta, 0.75)
+    layer = _ops.PrefillLayer(wl.q, wl.k, wl.v, tau, zmax)
+    out = layer.run()
+    torch.cuda.synchronize()
+    nb, hkv, d = 256, 8, 128
+    parts = np32(layer.tau_max)
+    assert parts.shape == (8, nb, hkv)
+    z = np32(layer.zeta)
+    mask = O.mask_from_scores(O.nanmax_axis0(parts), z, tau, zmax)
+    order, n = O.stream_compact_indices(mask)
+    assert n == int(layer.num_active[0]) == 64
+    np.testing.assert_array_equal(np32(layer.indices).astype(np.int64), order)
+    kk = wl.k.reshape(nb, 512, hkv, d)
+    qn = np32(wl.q)
+    for b in sorted({0, int(order[0]), int(order[n - 1]), int(order[n]), nb - 1}):
+        kb = np32(kk[b])
+        bounds = O.query_aware_bounds(qn, kb)[:, 0, :]          # (512 queries, hkv)
+        np.testing.assert_allclose(parts[:, b, :], bounds.reshape(8, 64, hkv).max(axis=1), rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(z[b], O.spectral_decay_ratio(kb)[0], rtol=1e-5)
+    rows = np.sort(np.random.default_rng(4).choice(512, 16, replace=False))
+    sel = torch.from_numpy(order[:n].astype(np.int64)).to(dev)
+    k_act = kk.index_select(0, sel).reshape(n * 512, hkv, d)
+    v_act = wl.v.reshape(nb, 512, hkv, d).index_select(0, sel).reshape(n * 512, hkv, d)
+    ref = O.attention_active_blocks(qn[rows], np32(k_act), np32(v_act), range(n))
+    close(np32(out[rows]), ref, 1e-2)
+    # a second run of the layer reproduces the first bit for bit
+    again = layer.run().clone()
+    torch.cuda.synchronize()
+    assert torch.equal(again, out)

@@ -228,3 +228,57 @@ def test_layer_logits_choice_matches_library(lib, kv, qf32, d, nq):
     assert full - cached == (logit_bytes if uses else 0)
     if kv == "bf16" and nq <= 4 and d <= 256:
         assert uses
+
+
+def test_unaligned_workspace_rejected(lib):
+    """A workspace that is not 256-byte aligned is refused before any launch
+    (the kernels read it with 16-byte vector loads at 256-byte offsets)."""
+    from orthocache_amd import _native as N
+
+    a = _plan_args(1, 32, 16, 256, 1, nb=128)
+    need = int(lib.oc_attend_workspace_size(C.byref(a)))
+    assert need > 0
+    base = 1 << 24
+    assert lib.oc_attend(C.byref(a), base + 16, need + 256, None) == -1
+    assert b"256-byte aligned" in lib.oc_last_error()
+    la = N.LayerArgs()
+    for f in ("q", "k", "v", "out"):
+        setattr(la, f, 1 << 20)
+    la.q_dtype = la.kv_dtype = la.out_dtype = 1
+    la.q_tok_stride = la.out_tok_stride = 32 * 256
+    la.q_head_stride = la.out_head_stride = la.k_head_stride = la.v_head_stride = 256
+    la.k_tok_stride = la.v_tok_stride = 16 * 256
+    la.head_dim, la.num_kv_heads, la.group, la.sq, la.total_blocks, la.num_segments = 256, 16, 2, 1, 128, 1
+    need = int(lib.oc_decode_layer_workspace_size(C.byref(la)))
+    assert need > 0
+    assert lib.oc_decode_layer(C.byref(la), base + 128, need + 256, None) == -1
+    assert b"256-byte aligned" in lib.oc_last_error()
+
+
+@pytest.mark.parametrize("nb,hkv,evict,seed", [(128, 16, 0.9, 0), (128, 16, 0.5, 1), (16, 1, 0.5, 2), (40, 3, 0.75, 3)])
+def test_calibrate_unified_thresholds_off_the_scores(nb, hkv, evict, seed):
+    """calibrate_unified (host-side, CPU tensors here) places tau strictly
+    between the K-th and (K+1)-th unified scores and zeta_max strictly between
+    two zeta values: the mask keeps exactly K blocks and no score equals a
+    threshold, so a restatement whose scores differ in the last bits keeps
+    the same blocks."""
+    import torch
+
+    from orthocache_amd import workloads
+
+    g = torch.Generator().manual_seed(seed)
+    tm = torch.randn(nb, hkv, generator=g) * 3 + 40
+    z = torch.rand(nb, hkv, generator=g) * 8
+    tau, zmax = workloads.calibrate_unified(tm, z, evict)
+    assert tau == float(np.float32(tau)) and zmax == float(np.float32(zmax))
+    tmn, zn = tm.numpy(), z.numpy()
+    assert not np.any(tmn == np.float32(tau)) and not np.any(zn == np.float32(zmax))
+    mask = O.mask_from_scores(tmn, zn, tau, zmax)
+    _, n = O.stream_compact_indices(mask)
+    assert n == int(round(nb * (1 - evict)))
+    # nudging every score by 4 ulps either way keeps the same mask
+    for direction in (np.inf, -np.inf):
+        nudged = tmn.copy()
+        for _ in range(4):
+            nudged = np.nextafter(nudged, np.float32(direction))
+        np.testing.assert_array_equal(O.mask_from_scores(nudged, zn, tau, zmax), mask)

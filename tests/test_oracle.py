@@ -185,14 +185,147 @@ class TestMasks:
         np.testing.assert_array_equal(m, [[True, False], [False, True]])
 
     def test_two_gate_reference_case(self):
-        # tests/test_spectral_bands.py:177-213 regenerated from its seed
+        # tests/test_spectral_bands.py:177-213 regenerated from its seed.  Block 0
+        # is white noise times the alternating sign: in natural order that
+        # multiplies by Walsh row 1, which only swaps coefficients s and s^1,
+        # so its spectrum stays flat (zeta ~ 256/63 like block 1's plain
+        # noise).  With tau = -100 and zeta_max = 1 both blocks fail gate 2:
+        # the exact mask is all False, which the reference's `not all()` allows.
         np.random.seed(42)
         keys = np.random.randn(1024, 1, 64).astype(np.float32)
         for i in range(512):
             keys[i, 0, :] *= (1.0 if i % 2 == 0 else -1.0) * 5.0
         q = np.random.randn(1, 1, 64).astype(np.float32)
         m = O.multiband_mask(q, keys, -100.0, 1.0)
-        assert m.shape == (2, 1) and not m.all()
+        np.testing.assert_array_equal(m, [[False], [False]])
+        z = O.spectral_decay_ratio(keys)[:, 0]
+        assert np.all((z > 2.5) & (z < 6.0)), z
+        # The swap s <-> s^1 moves only coefficient 1 into DC and DC into the
+        # low band; the high band of block 0 is the high band of the
+        # unmodulated noise, coefficient by coefficient.
+        raw = keys[:512, 0].astype(np.float64) * np.where(np.arange(512) % 2 == 0, 1.0, -1.0)[:, None]
+        spec_raw = H512 @ raw / np.sqrt(512)
+        spec_mod = H512 @ keys[:512, 0].astype(np.float64) / np.sqrt(512)
+        np.testing.assert_allclose(spec_mod[256:], spec_raw[np.arange(256, 512) ^ 1], rtol=1e-9, atol=1e-9)
+
+    def test_two_gate_separates_coherent_block(self):
+        # The same case with block 1 replaced by the reference's Walsh-coherent
+        # block (tests/test_spectral_bands.py:89-117: Walsh rows 1..15 with
+        # RandomState(42) * 0.5 coefficients, zeta < 0.01): gate 2 now keeps
+        # block 1 only, gate 1 at tau = -100 keeps both.
+        np.random.seed(42)
+        keys = np.random.randn(1024, 1, 64).astype(np.float32)
+        for i in range(512):
+            keys[i, 0, :] *= (1.0 if i % 2 == 0 else -1.0) * 5.0
+        q = np.random.randn(1, 1, 64).astype(np.float32)
+        rng = np.random.RandomState(42)
+        coh = np.zeros((512, 64))
+        for j in range(1, 16):
+            coh += np.outer(H512[:, j], rng.randn(64) * 0.5)
+        keys[512:, 0, :] = coh.astype(np.float32)
+        np.testing.assert_array_equal(O.multiband_mask(q, keys, -100.0, 1.0), [[False], [True]])
+        np.testing.assert_array_equal(O.query_aware_mask(q, keys, -100.0), [[True], [True]])
+        # gate 1 alone at a tau above every bound keeps nothing
+        np.testing.assert_array_equal(O.multiband_mask(q, keys, 1e6, 1.0), [[False], [False]])
+
+
+def walsh_keys(blocks, d):
+    """Keys whose spectra are known without a transform.
+
+    Each block is (m, a, c): K[t, :] = m + a w_1[t] s + c w_256[t] r, with
+    w_i the natural-order Walsh row i (Hadamard row i: w_1 alternates every
+    token, w_256 changes sign once, at token 256), m a (d,) mean vector and
+    s, r fixed +-1 vectors.  By orthogonality of the rows, per column the
+    transform (scaled 1/sqrt(512)) has coefficient 0 = sqrt(512) m,
+    coefficient 1 = sqrt(512) a s and coefficient 256 = sqrt(512) c r, so:
+    E_low = 512 a^2 d, E_mid = 0, E_high = 512 c^2 d, E_AC = 512 (a^2 + c^2) d,
+    kbar = m.
+    """
+    t = np.arange(512)
+    w1 = np.where(t % 2 == 0, 1.0, -1.0)
+    w256 = np.where(t < 256, 1.0, -1.0)
+    s = np.where(np.arange(d) % 3 == 0, -1.0, 1.0)
+    r = np.where(np.arange(d) % 2 == 0, 1.0, -1.0)
+    out = []
+    for m, a, c in blocks:
+        out.append(np.asarray(m, np.float64)[None, :] + a * np.outer(w1, s) + c * np.outer(w256, r))
+    return np.concatenate(out)[:, None, :]
+
+
+class TestWalshMasks:
+    """The mask entry points on keys whose scores follow from the construction.
+
+    q = [2, 0, 0, 0] (||q|| = 2, sqrt(d) = 2).  Blocks (m, a, c):
+      0: (0, 1, 0.5)         E_AC = 512*1.25*4 = 2560, tau = 0 + 2*sqrt(2560)/2 = 50.596, zeta = 0.25
+      1: (0, 0.5, 1)         tau = 50.596, zeta = 4
+      2: ([10,0,0,0], 1, .5) tau = 2*10/2 + 50.596 = 60.596, zeta = 0.25
+      3: ([-10,0,0,0], 1,.5) tau = -10 + 50.596 = 40.596, zeta = 0.25
+    """
+
+    Q = np.array([[[2.0, 0.0, 0.0, 0.0]]])
+    BLOCKS = [(np.zeros(4), 1.0, 0.5), (np.zeros(4), 0.5, 1.0), ([10.0, 0, 0, 0], 1.0, 0.5),
+              ([-10.0, 0, 0, 0], 1.0, 0.5)]
+
+    def test_scores_from_construction(self):
+        k = walsh_keys(self.BLOCKS, 4)
+        dc, lo, mi, hi = O.spectral_bands(k)
+        np.testing.assert_allclose(lo[:, 0], [512 * 4, 128 * 4, 512 * 4, 512 * 4], rtol=1e-12)
+        np.testing.assert_allclose(hi[:, 0], [128 * 4, 512 * 4, 128 * 4, 128 * 4], rtol=1e-12)
+        np.testing.assert_allclose(mi, 0, atol=1e-9)
+        # zeta = E_high / (E_low + 1e-6) (spectral_energy.py:138)
+        z_co, z_hi = 512.0 / (2048.0 + 1e-6), 2048.0 / (512.0 + 1e-6)
+        np.testing.assert_allclose(O.spectral_decay_ratio(k)[:, 0], [z_co, z_hi, z_co, z_co], rtol=1e-12)
+        e = np.sqrt(2560.0)
+        np.testing.assert_allclose(O.query_aware_bounds(self.Q, k)[0, :, 0], [e, e, 10 + e, -10 + e], rtol=1e-12)
+
+    def test_query_aware_mask(self):
+        k = walsh_keys(self.BLOCKS, 4)
+        np.testing.assert_array_equal(O.query_aware_mask(self.Q, k, 55.0)[:, 0], [False, False, True, False])
+        np.testing.assert_array_equal(O.query_aware_mask(self.Q, k, 45.0)[:, 0], [True, True, True, False])
+
+    def test_multiband_mask(self):
+        k = walsh_keys(self.BLOCKS, 4)
+        np.testing.assert_array_equal(O.multiband_mask(self.Q, k, 45.0, 1.0)[:, 0], [True, False, True, False])
+        np.testing.assert_array_equal(O.multiband_mask(self.Q, k, 45.0, 5.0)[:, 0], [True, True, True, False])
+        np.testing.assert_array_equal(O.multiband_mask(self.Q, k, 30.0, 0.1)[:, 0], [False, False, False, False])
+        # the max is over queries: a second query pointing the other way lifts block 3
+        q2 = np.concatenate([self.Q, -self.Q], axis=0)
+        np.testing.assert_array_equal(O.multiband_mask(q2, k, 55.0, 1.0)[:, 0], [False, False, True, True])
+
+    def test_planted_sequency_order_flips_gate_two(self):
+        # A sequency-ordered transform would put w_1 (511 sign changes) in the
+        # high band and w_256 (one sign change) in the low band, inverting zeta.
+        k = walsh_keys(self.BLOCKS, 4)
+        nat = O.run_fwht_on_blocks(k)
+        seq_idx = np.array([int(bin(i ^ (i >> 1))[2:].zfill(9)[::-1], 2) for i in range(512)])
+        spec = np.empty_like(nat)
+        spec[:, seq_idx] = nat  # natural index -> sequency index
+        bad_zeta = (spec[:, 256:] ** 2).sum(axis=(1, 3)) / ((spec[:, 1:64] ** 2).sum(axis=(1, 3)) + 1e-6)
+        bad = (O.query_aware_bounds(self.Q, k).max(0) >= 45.0) & (bad_zeta <= 1.0)
+        assert list(bad[:, 0]) != [True, False, True, False]
+
+
+class TestAutoTau:
+    def test_known_answer(self):
+        # mean 2.5, population variance 1.25 (ddof=0, jnp.std's default)
+        assert O.auto_tau_from_max_bounds([[1.0, 2.0], [3.0, 4.0]]) == pytest.approx(2.5 - np.sqrt(1.25), rel=1e-15)
+        assert O.auto_tau_from_max_bounds(np.full((3, 2), 7.0)) == 7.0
+
+    def test_planted_sample_std_fails(self):
+        bad = 2.5 - np.std([1.0, 2.0, 3.0, 4.0], ddof=1)
+        assert bad != pytest.approx(O.auto_tau_from_max_bounds([1.0, 2.0, 3.0, 4.0]), rel=1e-6)
+
+    def test_walsh_construction(self):
+        # max bounds of TestWalshMasks: [e, e, 10 + e, -10 + e] with e = sqrt(2560):
+        # mean e + 0, population std sqrt((0 + 0 + 100 + 100) / 4) = sqrt(50).
+        k = walsh_keys(TestWalshMasks.BLOCKS, 4)
+        assert O.auto_tau(TestWalshMasks.Q, k) == pytest.approx(np.sqrt(2560.0) - np.sqrt(50.0), rel=1e-12)
+        # the max runs over queries before the statistics (pipeline.py:173)
+        q2 = np.concatenate([TestWalshMasks.Q, -TestWalshMasks.Q], axis=0)
+        e = np.sqrt(2560.0)
+        mb = [e, e, 10 + e, 10 + e]
+        assert O.auto_tau(q2, k) == pytest.approx(np.mean(mb) - np.sqrt(np.mean((np.array(mb) - np.mean(mb)) ** 2)),
+                                                   rel=1e-12)
 
     def test_fp32_threshold_rounding_and_nan(self):
         tau = 0.1  # not representable: JAX compares against fp32(0.1)
@@ -365,12 +498,29 @@ class TestPlantedMistakes:
         assert abs(y[511]) < 1e-9 and abs(y[1]) > 1
 
     def test_unstable_partition_fails_kat(self):
+        # A two-pointer (Hoare) partition puts the same blocks first but not in
+        # order: the KAT of tests/test_alltoallv.py:60-67 must reject it.
         m = np.array([False, True, False, True, True, False])
-        bad = np.argsort(-m.astype(int), kind="quicksort")
-        good, _ = O.stream_compact_indices(m)
-        # a non-stable sort need not give the reference order; the KAT pins it
-        assert list(good[:3]) == [1, 3, 4]
-        assert sorted(bad[:3]) == [1, 3, 4]
+
+        def hoare(mask):
+            order = list(range(len(mask)))
+            i, j = 0, len(mask) - 1
+            while True:
+                while i < j and mask[order[i]]:
+                    i += 1
+                while i < j and not mask[order[j]]:
+                    j -= 1
+                if i >= j:
+                    return np.array(order), int(mask.sum())
+                order[i], order[j] = order[j], order[i]
+
+        def kat_ok(order, n):
+            return n == 3 and list(order[:3]) == [1, 3, 4] and list(order[3:]) == [0, 2, 5]
+
+        bad, nb = hoare(m)
+        assert sorted(bad[:nb]) == [1, 3, 4]  # the right set ...
+        assert not kat_ok(bad, nb)            # ... in the wrong order
+        assert kat_ok(*O.stream_compact_indices(m))
 
     def test_wrong_sqrt_d_fails_closed_form(self):
         rng = np.random.default_rng(15)
