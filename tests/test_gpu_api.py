@@ -129,14 +129,18 @@ def test_masks_c2_shape(dev, evict):
     sc = _ops.score(wl.k, wl.q)
     tm, z = np32(sc.tau_max[0]), np32(sc.zeta)
     tau = gap_threshold(tm, evict)
-    zmax = gap_threshold(z, 0.6)  # gate 2 evicts ~40% of the entries, so both gates bite
+    zmax = gap_threshold(z, 0.6)  # gate 2 evicts ~40% of the entries
     qa = oc.compute_query_aware_mask(wl.q, wl.k, tau)
     mb = oc.compute_multiband_mask(wl.q, wl.k, tau, zmax)
     torch.cuda.synchronize()
     assert qa.dtype == torch.bool and tuple(qa.shape) == (128, 16)
     np.testing.assert_array_equal(np32(qa).astype(bool), O.mask_from_scores(tm, np.zeros_like(z), tau, 0.0))
     np.testing.assert_array_equal(np32(mb).astype(bool), O.mask_from_scores(tm, z, tau, zmax))
-    assert 0 < np32(mb).sum() < np32(qa).sum() < qa.numel()
+    assert 0 < np32(mb).sum() <= np32(qa).sum() < qa.numel()
+    if evict == 0.5:
+        # both gates bite (at 90% eviction the kept tiles are the noise-injected
+        # blocks, whose energy sits in the low band: gate 2 passes them all)
+        assert np32(mb).sum() < np32(qa).sum()
     # the float64 oracle agrees on sampled blocks
     kk = wl.k.reshape(128, 512, 16, 256)
     qf = O.fold_gqa(np32(wl.q), 16)
