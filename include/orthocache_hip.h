@@ -354,6 +354,26 @@ size_t oc_decode_layer_cached_workspace_size(const oc_layer_args* a);
 int oc_decode_layer_cached(const oc_layer_args* a, const oc_block_stats* stats, void* workspace,
                            size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------- allocation-free decode layer
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory -- code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc: oc_decode_layer without a workspace argument.  The
+ * library keeps OC_NOALLOC_SCRATCH_BYTES of scratch memory on every GPU it
+ * runs on (a static device array, loaded with the library and held until the
+ * process ends) and runs the layer there; inputs and outputs are the
+ * caller's, as for oc_decode_layer, with the same results.  The call
+ * allocates nothing; its first call on a device looks up that device's
+ * scratch address.  A layer whose oc_decode_layer_workspace_size() exceeds
+ * the scratch is rejected with OC_ERR_WORKSPACE before any launch (C2 --
+ * 64K tokens, 16 kv heads, head_dim 256, two query rows per kv head -- needs
+ * 10 MiB; 128K tokens 18 MiB).  The stream must belong to the current
+ * device.  Every call on one GPU uses that GPU's scratch: calls that overlap
+ * on one GPU (several streams or threads) race, and the caller must
+ * serialise them.  Each call writes every scratch byte it reads, so nothing
+ * has to be cleared between calls. */
+#define OC_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int oc_decode_layer_noalloc(const oc_layer_args* a, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -98,8 +98,10 @@ EXPORTED_SYMBOLS = (
     "oc_score_blocks", "oc_query_bounds", "oc_query_bound_tiles", "oc_mask_compact",
     "oc_copy_blocks", "oc_attend_workspace_size", "oc_attend", "oc_attend_plan",
     "oc_decode_layer_workspace_size", "oc_decode_layer",
-    "oc_decode_layer_cached_workspace_size", "oc_decode_layer_cached",
+    "oc_decode_layer_cached_workspace_size", "oc_decode_layer_cached", "oc_decode_layer_noalloc",
 )
+
+NOALLOC_SCRATCH_BYTES = 32 << 20  # OC_NOALLOC_SCRATCH_BYTES
 
 _lib = None
 
@@ -127,6 +129,7 @@ def lib() -> C.CDLL:
         ("oc_attend", [C.POINTER(AttendArgs), _vp, C.c_size_t, _vp]),
         ("oc_attend_plan", [C.POINTER(AttendArgs), C.POINTER(_i32), C.POINTER(_i32)]),
         ("oc_decode_layer", [C.POINTER(LayerArgs), _vp, C.c_size_t, _vp]),
+        ("oc_decode_layer_noalloc", [C.POINTER(LayerArgs), _vp]),
     ):
         f = getattr(L, name)
         f.argtypes = argt

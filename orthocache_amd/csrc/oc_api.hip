@@ -1,5 +1,6 @@
 // C ABI of liborthocache_hip.so: argument validation, workspace layout and
 // kernel launches.  Declarations and semantics: include/orthocache_hip.h.
+#include "oc_api_internal.h"
 #include "oc_kernels.h"
 #include "orthocache_hip.h"
 
@@ -543,3 +544,22 @@ int oc_decode_layer_cached(const oc_layer_args* a, const oc_block_stats* stats, 
 }
 
 }  // extern "C"
+
+namespace oc {
+
+int api_fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int api_hip_check(hipError_t e, const char* what) { return hip_check(e, what); }
+
+int decode_layer_run(const oc_layer_args* a, void* workspace, size_t workspace_bytes, void* stream,
+                     const char* name) {
+  return decode_layer_impl(a, nullptr, workspace, workspace_bytes, stream, name);
+}
+
+}  // namespace oc

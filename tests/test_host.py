@@ -255,6 +255,32 @@ def test_unaligned_workspace_rejected(lib):
     assert b"256-byte aligned" in lib.oc_last_error()
 
 
+def test_noalloc_rejects_layers_beyond_its_scratch(lib):
+    """oc_decode_layer_noalloc refuses, before any launch or device call, a
+    layer whose workspace exceeds the library's fixed scratch (here C2's shape
+    at 512K tokens: 67 MB of scoring-pass logits alone)."""
+    from orthocache_amd import _native as N
+
+    la = N.LayerArgs()
+    for f in ("q", "k", "v", "out"):
+        setattr(la, f, 1 << 20)
+    la.q_dtype = la.kv_dtype = la.out_dtype = 1
+    la.q_tok_stride = la.out_tok_stride = 32 * 256
+    la.q_head_stride = la.out_head_stride = la.k_head_stride = la.v_head_stride = 256
+    la.k_tok_stride = la.v_tok_stride = 16 * 256
+    la.head_dim, la.num_kv_heads, la.group, la.sq, la.num_segments = 256, 16, 2, 1, 1
+    la.total_blocks = 1024
+    need = int(lib.oc_decode_layer_workspace_size(C.byref(la)))
+    assert need > N.NOALLOC_SCRATCH_BYTES
+    assert lib.oc_decode_layer_noalloc(C.byref(la), None) == -4
+    msg = lib.oc_last_error()
+    assert b"scratch" in msg and str(need).encode() in msg
+    # C2 at 64K tokens fits
+    la.total_blocks = 128
+    assert 0 < int(lib.oc_decode_layer_workspace_size(C.byref(la))) <= N.NOALLOC_SCRATCH_BYTES
+    assert lib.oc_decode_layer_noalloc(None, None) == -1
+
+
 @pytest.mark.parametrize("nb,hkv,evict,seed", [(128, 16, 0.9, 0), (128, 16, 0.5, 1), (16, 1, 0.5, 2), (40, 3, 0.75, 3)])
 def test_calibrate_unified_thresholds_off_the_scores(nb, hkv, evict, seed):
     """calibrate_unified (host-side, CPU tensors here) places tau strictly
