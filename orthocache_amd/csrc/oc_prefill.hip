@@ -20,18 +20,20 @@
 //   S^T = K Q^T   A = K tile rows from LDS (16 B per lane), B = Q^T slice from
 //                 registers (loaded once), C lane l, i -> key 8(i/4)+4(l/32)+i%4,
 //                 query l%32;
-//   O^T += V^T P^T  A = V^T from a transposed LDS copy, B = P^T straight from
-//                 the S^T registers (converted to bf16/fp16), C -> d, query l%32.
+//   O^T += V^T P^T  A = V^T read from the natural V tile with the transposing
+//                 LDS read ds_read_b64_tr_b16, B = P^T straight from the S^T
+//                 registers (converted to bf16/fp16), C -> d, query l%32.
 // So every query's softmax state (m, l) and its column of O^T stay in the two
 // lanes that own the query: no shuffles except one xor-32 per tile for the row
 // max.  The MFMA k index of P^T / V^T is a permutation of the 16 keys of a
-// slice (the keys a lane holds in S^T); the V^T copy in LDS stores keys in that
-// order so the A operand is one 16-byte read.
+// slice (the keys a lane holds in S^T); the transposing reads fetch V's keys
+// in that order.
 //
-// LDS: K tile [64 keys][D] and V^T tile [D][64 keys], both with 16-byte blocks
-// XOR-swizzled by row so operand reads and the transposing writes spread over
-// the banks.  Global loads of the next tile are issued into registers before
-// the current tile's arithmetic.
+// LDS: three K tiles [64 keys][D] and three V tiles [64 keys][D], both
+// loaded straight from global memory (global_load_lds), 16-byte blocks
+// XOR-swizzled by row so the operand reads spread over the banks.  At tile
+// step j the loads of K_{j+3} and V_{j+2} are issued while K_{j+1} and V_j
+// are read, so every load has two steps to land.
 #include "oc_kernels.h"
 
 namespace oc {
@@ -80,23 +82,44 @@ __device__ __forceinline__ u32x4_t ld16v(const char* p) {
   return *reinterpret_cast<const u32x4_t*>(p);
 }
 
-// Position of key k (0..63) of a tile in the V^T rows: the 8 keys that lane
-// half hf supplies for MFMA k-slice s of S^T tile t are contiguous.
-__host__ __device__ constexpr int vt_pos(int k) {
-  const int t = k >> 5, s = (k >> 4) & 1, r = k & 15;
-  const int hf = (r >> 2) & 1, j = ((r >> 3) << 2) | (r & 3);
-  return (((t * 2 + s) * 2 + hf) << 3) | j;
-}
-
 // Swizzled byte offset of 16-byte block `blk` of row `row`.
 template <int ROW_BYTES>
 __device__ __forceinline__ int k_off(int row, int blk) {
   constexpr int mask = (ROW_BYTES / 16 < 16 ? ROW_BYTES / 16 : 16) - 1;
   return row * ROW_BYTES + ((blk ^ (row & mask)) << 4);
 }
-__device__ __forceinline__ int vt_off(int row, int byte_in_row) {
-  const int blk = byte_in_row >> 4;
-  return row * (kPfKeys * 2) + (((blk ^ ((row + (row >> 3)) & 7)) << 4) | (byte_in_row & 15));
+
+// Swizzle of the natural V tile in LDS: 16-byte block b of key row r sits at
+// position b ^ vt_swizzle(r).  The transposing operand reads of one MFMA take
+// 8 rows (row & 3 = 0..3, twice) x 64 bytes; with these swizzles they cover
+// every bank exactly twice (rows of 256 bytes for head_dim 128; of 128 bytes,
+// two to a bank row, for 64).
+template <int D>
+__host__ __device__ constexpr int vt_swizzle(int r) {
+  return D == 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1);
+}
+
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: the 64-bit transposing LDS read of gfx950.
+__device__ __forceinline__ v4i16_t ld_tr16(const char* lds_byte_addr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t*)(lds_byte_addr));
+}
+
+// s_waitcnt operand: vmcnt <= 4, expcnt and lgkmcnt not waited for.
+constexpr unsigned kVmcntLe4 = 4u | (7u << 4) | (15u << 8);
+
+// A global -> LDS load of 16 bytes per lane (global_load_lds_dwordx4: lane l
+// writes 16 bytes at LDS address m0 + 16 l), written as inline assembly so
+// that the compiler does not track its LDS write.  It cannot tell the six
+// tile buffers apart and would otherwise wait for every load in flight
+// (vmcnt(0)) before each step's LDS reads; the kernel orders these loads
+// itself (s_waitcnt vmcnt, a barrier per step, vmcnt(0) before it ends).
+// One wait state separates the M0 write from the load.
+__device__ __forceinline__ void g2lds16(const void* gaddr, const void* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gaddr), "s"(m0) : "memory", "m0");
 }
 
 }  // namespace
@@ -126,22 +149,23 @@ __global__ __launch_bounds__(kPfMaxThreads, 2) void attend_prefill_kernel(Attend
   constexpr int kPfRows = prefill_tile_rows(D);
   constexpr int DS = D / 16;                 // d slices of Q K^T
   constexpr int DTN = D / 32;                // 32-row d tiles of O^T
-  constexpr int KROW = D * 2;                // bytes per K row in LDS
-  constexpr int KCH = kPfKeys * D / 8 / kPfThreads;  // 16-byte K chunks per thread
-  constexpr int KPT = kPfKeys * (D / 8) / kPfThreads;  // keys per thread in the V transpose (2)
+  constexpr int KROW = D * 2;                // bytes per K / V row in LDS
   constexpr int NDCH = D / 8;                // 16-byte chunks per row
-  static_assert(KCH >= 1 && (KPT == 2 || KPT == 4), "unsupported head_dim");
+  constexpr int KCH = kPfKeys * NDCH / kPfThreads;  // 16-byte chunks per thread of a K or V tile
+  static_assert(KCH == 2, "two 16-byte chunks of K and two of V per thread and tile");
+  constexpr int TBYTES = kPfKeys * KROW;     // one K or V tile in LDS
 
-  constexpr int KBYTES = kPfKeys * KROW;     // one K tile in LDS
-  constexpr int VBYTES = D * kPfKeys * 2;    // one V^T tile in LDS
-  // Two buffers each (separate objects, so the compiler sees that loads into
-  // one never alias reads of the other): while tile j's softmax and P V run,
-  // tile j+1's K is already in LDS for its Q K^T, and K_{j+2} and V_{j+1} go
-  // to the buffers tile j-1 has released -- one barrier per tile.
-  __shared__ __align__(16) char s_k0[KBYTES];
-  __shared__ __align__(16) char s_k1[KBYTES];
-  __shared__ __align__(16) char s_v0[VBYTES];
-  __shared__ __align__(16) char s_v1[VBYTES];
+  // Three buffers each, as separate objects, so the compiler sees that the
+  // direct-to-LDS loads into one never alias reads of another.  At tile step
+  // j, K_{j+1} (for S_{j+1}) and V_j (for P_j V_j) are read while K_{j+2} and
+  // V_{j+1} are in flight and K_{j+3} and V_{j+2} are requested into the
+  // buffers that K_j and V_{j-1} released: every load has two steps to land.
+  __shared__ __align__(16) char s_k0[TBYTES];
+  __shared__ __align__(16) char s_k1[TBYTES];
+  __shared__ __align__(16) char s_k2[TBYTES];
+  __shared__ __align__(16) char s_v0[TBYTES];
+  __shared__ __align__(16) char s_v1[TBYTES];
+  __shared__ __align__(16) char s_v2[TBYTES];
 
   const int nq_rows = prefill_rows(p);
   const int nqt = (nq_rows + kPfRows - 1) / kPfRows;
@@ -196,43 +220,27 @@ __global__ __launch_bounds__(kPfMaxThreads, 2) void attend_prefill_kernel(Attend
   const char* kbase = reinterpret_cast<const char*>(p.k) + (int64_t)h * p.k_head_stride * 2;
   const char* vbase = reinterpret_cast<const char*>(p.v) + (int64_t)h * p.v_head_stride * 2;
 
-  // This thread's share of a tile: K chunks c = t + kPfThreads u, loaded straight
+  // This thread's share of a tile: chunks c = t + kPfThreads u, loaded straight
   // into LDS (lane l of a wave writes 16 bytes at the instruction's base +
   // 16 l), so LDS chunk c -- row c / NDCH, swizzled position c % NDCH -- is
-  // fetched from the global chunk the swizzle puts there; V keys
-  // vk0 .. vk0 + KPT - 1 at chunk vdch, through registers for the transpose.
-  // Lane -> (16-byte chunk, key group) of the V transpose (two keys per
-  // thread, one 4-byte write per dim).  For head_dim 128 the 32 lanes of an
-  // LDS write phase cover 8 dims (8 rows of V^T, whose swizzles differ) x the
-  // 4 key pairs of one 16-byte block position, i.e. 32 distinct banks; a
-  // wave still reads whole 256-byte key rows.  (The previous map put only 8
-  // banks under a phase: 16% bank-conflict cycles, no measurable time.)
-  int vdch, vgrp;
-  if constexpr (NDCH == 16) {
-    static_assert(kPfThreads == 512 && KPT == 2, "lane map for 512 threads, two keys each");
-    vdch = (t & 7) | (((t >> 5) & 1) << 3);
-    vgrp = ((t >> 3) & 1) | (((t >> 6) & 1) << 1) | (((t >> 4) & 1) << 2) | (((t >> 7) & 3) << 3);
-  } else {
-    vdch = t % NDCH;
-    vgrp = t / NDCH;
-  }
-  const int vk0 = vgrp * KPT;
-  // Byte offsets inside a tile (64 token rows), fixed per thread.
-  int koff[KCH], voff[KPT];
+  // fetched from the global chunk the swizzle puts there.  K blocks are
+  // XOR-swizzled by row & 15 (conflict-free 16-byte operand reads); V blocks
+  // by vt_swizzle (conflict-free transposing operand reads, below).
+  int koff[KCH], voff[KCH];
 #pragma unroll
   for (int u = 0; u < KCH; ++u) {
     const int c = t + kPfThreads * u;
     constexpr int mask = (NDCH < 16 ? NDCH : 16) - 1;
     const int r = c / NDCH;
     koff[u] = (int)(r * krow_g) + (((c % NDCH) ^ (r & mask)) << 4);
+    voff[u] = (int)(r * vrow_g) + (((c % NDCH) ^ vt_swizzle<D>(r)) << 4);
   }
-#pragma unroll
-  for (int i = 0; i < KPT; ++i) voff[i] = (int)((vk0 + i) * vrow_g) + vdch * 16;
-  // First token of the split's tile j.  List and page entries are read with
-  // scalar loads (the tile is the same for the whole workgroup), which do not
-  // wait behind the tile loads in flight.
+  // First token of the split's tile j (clamped to the last tile: the loads
+  // past the end re-read it into buffers that are never consumed).  List and
+  // page entries are read with scalar loads (the tile is the same for the
+  // whole workgroup), which do not wait behind the tile loads in flight.
   auto tile_tok = [&](int j) -> int64_t {
-    const int tau = t0 + j;
+    const int tau = t0 + min(j, n - 1);
     const int blk = min(max(ld_const(idx + tau / tpb), 0), nbs - 1);
     int64_t page = (int64_t)off + blk;
     if (p.pages) {
@@ -241,42 +249,16 @@ __global__ __launch_bounds__(kPfMaxThreads, 2) void attend_prefill_kernel(Attend
     }
     return page * p.block_size + (int64_t)(tau % tpb) * kPfKeys;
   };
-  u32x4_t vr[KPT];
   const int wbase = __builtin_amdgcn_readfirstlane(wave) * kWave * 16;
   auto load_k = [&](int64_t tok, char* sk) {
     const char* kt = kbase + tok * krow_g;
 #pragma unroll
-    for (int u = 0; u < KCH; ++u)
-      __builtin_amdgcn_global_load_lds((const void*)(kt + koff[u]),
-                                       (__attribute__((address_space(3))) void*)(sk + u * kPfThreads * 16 + wbase),
-                                       16, 0, 0);
+    for (int u = 0; u < KCH; ++u) g2lds16(kt + koff[u], sk + u * kPfThreads * 16 + wbase);
   };
-  auto load_v = [&](int64_t tok) {
+  auto load_v = [&](int64_t tok, char* sv) {
     const char* vt = vbase + tok * vrow_g;
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) vr[i] = ld16v(vt + voff[i]);
-  };
-  // V^T: element e of the chunk is dim 8 vdch + e; the KPT keys are adjacent
-  // in vt_pos order, so each dim takes one 4- or 8-byte write.
-  auto store_v = [&](char* sv) {
-    const int pb = vt_pos(vk0) * 2;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int w = e >> 1;
-      const bool hi = e & 1;
-      uint32_t pk[KPT / 2];
-#pragma unroll
-      for (int i = 0; i < KPT / 2; ++i) {
-        const uint32_t a = vr[2 * i][w], b = vr[2 * i + 1][w];
-        pk[i] = hi ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
-      }
-      char* dst = sv + vt_off(8 * vdch + e, pb);
-      if constexpr (KPT == 4) {
-        *reinterpret_cast<uint2*>(dst) = make_uint2(pk[0], pk[1]);
-      } else {
-        *reinterpret_cast<uint32_t*>(dst) = pk[0];
-      }
-    }
+    for (int u = 0; u < KCH; ++u) g2lds16(vt + voff[u], sv + u * kPfThreads * 16 + wbase);
   };
   // S^T for the two 32-key halves of a tile, the two MFMA chains interleaved
   // over the d slices.
@@ -294,6 +276,24 @@ __global__ __launch_bounds__(kPfMaxThreads, 2) void attend_prefill_kernel(Attend
     s[0] = acc0;
     s[1] = acc1;
   };
+  // V^T operands by transposing reads of the natural V tile.  The P V
+  // product takes, at slice s (keys 16 s .. 16 s + 15), lane l's 8 keys
+  // 16 s + 8 (j / 4) + 4 hf + j % 4 (j = 0..7: the keys lane l holds in S^T)
+  // of dim 32 dt + l % 32.  ds_read_b64_tr_b16 gives lane i of a 16-lane
+  // group element i % 4 of the rows addressed by lanes i / 4 + 4 e (e = 0..3)
+  // (pinned by an in-bounds probe on the box), so when group lane 4 m + a
+  // addresses row kb + m, dims base + 4 a .. + 3, lane i receives keys kb ..
+  // kb + 3 of dim base + i: two reads (kb = 16 s + 4 hf and 16 s + 8 + 4 hf)
+  // form the operand.  Rows 16 s + 8 rr + 4 hf + m all have row & 3 = m, so
+  // the lane's swizzled offset is fixed per d tile.
+  int vt_lane[DTN];
+  {
+    const int m4 = (lane & 15) >> 2, a = lane & 3, g1 = (lane >> 4) & 1;
+    const int lane_base = (4 * hf + m4) * KROW + 32 * g1 + 8 * a;
+    const int sw = vt_swizzle<D>(m4) >> 2;  // the swizzle of rows with row & 3 = m4, in units of 4 blocks
+#pragma unroll
+    for (int dt = 0; dt < DTN; ++dt) vt_lane[dt] = lane_base + 64 * (dt ^ sw);
+  }
 
   f32x16_t o[DTN];
 #pragma unroll
@@ -303,34 +303,33 @@ __global__ __launch_bounds__(kPfMaxThreads, 2) void attend_prefill_kernel(Attend
   float m_run = -INFINITY, l_run = 0.f;
   const float c = p.logit_scale;
 
-  // Prologue: K_0, K_1 and V_0 in LDS, V_1 in registers, S_0.  Every
-  // direct-to-LDS load has completed before the barrier that publishes it.
+  // Prologue: K_0, K_1, K_2 and V_0, V_1 requested, all landed before S_0.
   f32x16_t s_cur[2], s_nxt[2];
-  int64_t tok2 = 0;  // first token of tile j+2 at step j
+  int64_t tok_k = 0, tok_v = 0;  // tiles to request at the next step: K_{j+3}, V_{j+2}
   if (n > 0) {
-    const int64_t tok0 = tile_tok(0);
+    const int64_t tok0 = tile_tok(0), tok1 = tile_tok(1), tok2 = tile_tok(2);
     load_k(tok0, s_k0);
-    const int64_t tok1 = n > 1 ? tile_tok(1) : tok0;
-    if (n > 1) load_k(tok1, s_k1);
-    load_v(tok0);
-    store_v(s_v0);
-    if (n > 1) load_v(tok1);
-    if (n > 2) tok2 = tile_tok(2);
+    load_k(tok1, s_k1);
+    load_k(tok2, s_k2);
+    load_v(tok0, s_v0);
+    load_v(tok1, s_v1);
+    tok_v = tok2;
+    tok_k = tile_tok(3);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     qk(s_k0, s_cur);
   }
-  // Tile j: K_j was read by the previous tile's step, V_j and K_{j+1} are in
-  // LDS.  kf / vn: the buffers to fill (K_{j+2}, V_{j+1}); kn / sv: K_{j+1}
-  // and V_j.  Past the end the V store writes stale registers into a buffer
-  // that is never read again, and qk computes an S that is never used.
-  auto step = [&](int j, char* kf, const char* kn, char* vn, const char* sv) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (j + 2 < n) load_k(tok2, kf);
-    store_v(vn);
-    if (j + 2 < n) load_v(tok2);
-    if (j + 3 < n) tok2 = tile_tok(j + 3);
+  // Tile step j: kc holds K_{j+1}, vc V_j; kf and vf (K_j's and V_{j-1}'s
+  // buffers) receive K_{j+3} and V_{j+2}.  Each step requests exactly four
+  // 16-byte loads per thread, so waiting until at most four are outstanding
+  // lands everything requested before the previous step.
+  auto step = [&](int j, char* kf, const char* kc, char* vf, const char* vc) {
+    if (j > 0) __builtin_amdgcn_s_waitcnt(kVmcntLe4);
+    lds_barrier();
+    load_k(tok_k, kf);
+    load_v(tok_v, vf);
+    tok_v = tok_k;
+    tok_k = tile_tok(j + 4);
 
     // Online softmax of tile j for query q32 (both lane halves hold it).
     float mx = -INFINITY;
@@ -357,7 +356,7 @@ __global__ __launch_bounds__(kPfMaxThreads, 2) void attend_prefill_kernel(Attend
     // S_{j+1} (independent of this tile's softmax, so its MFMAs overlap the
     // exponentials below; the rescale branch comes first so that both are in
     // one basic block).
-    qk(kn, s_nxt);
+    qk(kc, s_nxt);
     // P^T slices for the P V product, packed to the MFMA operand type as they
     // are made; the row sum adds the packed weights (what P V multiplies).
     float psum = 0.f;
@@ -376,27 +375,33 @@ __global__ __launch_bounds__(kPfMaxThreads, 2) void attend_prefill_kernel(Attend
 
     // O^T += V^T P^T over the four 16-key slices.
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
+    for (int s4 = 0; s4 < 4; ++s4) {
+      u32x4_t va[DTN];
 #pragma unroll
-      for (int sl = 0; sl < 2; ++sl) {
-        const int pb = (((kt * 2 + sl) * 2 + hf) << 4);
-        u32x4_t va[DTN];
-#pragma unroll
-        for (int dt = 0; dt < DTN; ++dt) va[dt] = *reinterpret_cast<const u32x4_t*>(sv + vt_off(dt * 32 + q32, pb));
-        const u32x4_t b = pb4[kt * 2 + sl];
-#pragma unroll
-        for (int dt = 0; dt < DTN; ++dt) o[dt] = M::run(va[dt], b, o[dt]);
+      for (int dt = 0; dt < DTN; ++dt) {
+        const v4i16_t r0 = ld_tr16(vc + 16 * s4 * KROW + vt_lane[dt]);
+        const v4i16_t r1 = ld_tr16(vc + (16 * s4 + 8) * KROW + vt_lane[dt]);
+        const uint2 w0 = __builtin_bit_cast(uint2, r0), w1 = __builtin_bit_cast(uint2, r1);
+        va[dt] = u32x4_t{w0.x, w0.y, w1.x, w1.y};
       }
+      const u32x4_t b = pb4[s4];
+#pragma unroll
+      for (int dt = 0; dt < DTN; ++dt) o[dt] = M::run(va[dt], b, o[dt]);
     }
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) s_cur[kt] = s_nxt[kt];
   };
-  for (int j = 0; j < n; j += 2) {
-    step(j, s_k0, s_k1, s_v1, s_v0);
-    if (j + 1 < n) step(j + 1, s_k1, s_k0, s_v0, s_v1);
+  for (int j = 0; j < n; j += 3) {
+    step(j, s_k0, s_k1, s_v2, s_v0);
+    if (j + 1 < n) step(j + 1, s_k1, s_k2, s_v0, s_v1);
+    if (j + 2 < n) step(j + 2, s_k2, s_k0, s_v1, s_v2);
   }
+  // The last steps' loads (re-reads of the last tile) land before the
+  // workgroup can release its LDS.
+  __builtin_amdgcn_s_waitcnt(0);
 
-  // Partial for this split: m and l per row, O^T unnormalised.
+  // Partial for this split: m and l per row, O^T unnormalised ([D][rows]
+  // per slab, so each store of a wave writes two 128-byte row runs).
   const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
   const int64_t rows_pad = (int64_t)nqt * kPfRows;
   const int64_t slab = ((int64_t)(split * p.num_segments + seg) * p.num_kv_heads + h);
