@@ -276,6 +276,27 @@ def test_orthocache_attention_partitioned(dev):
     assert torch.equal(out, ref)
 
 
+def test_orthocache_attention_partitioned_head_shards(dev):
+    """partitioning.py:20-50's sharding rule 'q h d, k h d, k h d, b h -> q h d':
+    with two head shards each shard compacts over its own kv head's mask, so
+    shard 0 (q heads 0-1, kv head 0) attends blocks {0, 4} and shard 1 (q heads
+    2-3, kv head 1) blocks {2, 4}; uneven splits are refused."""
+    import orthocache_amd as oc
+
+    q, k, v = _qkv(dev, 6, 3, 4, 2, 64, torch.float32, seed=9)
+    m = torch.tensor([[True, False], [False, False], [False, True], [False, False], [True, True], [False, False]],
+                     device=dev)
+    out = oc.orthocache_attention_partitioned(q, k, v, m, num_shards=2)
+    assert out.dtype == torch.float32 and out.shape == q.shape
+    qn, kn, vn = np32(q), np32(k), np32(v)
+    close(np32(out[:, :2]), O.attention_active_blocks(qn[:, :2], kn[:, :1], vn[:, :1], [0, 4]), 1e-4)
+    close(np32(out[:, 2:]), O.attention_active_blocks(qn[:, 2:], kn[:, 1:], vn[:, 1:], [2, 4]), 1e-4)
+    whole = oc.orthocache_attention_partitioned(q, k, v, m, num_shards=1)
+    assert not torch.equal(out, whole)
+    with pytest.raises(ValueError, match="split evenly"):
+        oc.orthocache_attention_partitioned(q, k, v, m, num_shards=3)
+
+
 def test_forward_sparse_mode_output(dev):
     """orthocache_forward(mode='sparse') (pipeline.py:146-148): each head
     attends its own kept blocks; a head keeping none returns zeros (the gated

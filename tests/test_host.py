@@ -308,3 +308,19 @@ def test_calibrate_unified_thresholds_off_the_scores(nb, hkv, evict, seed):
         for _ in range(4):
             nudged = np.nextafter(nudged, np.float32(direction))
         np.testing.assert_array_equal(O.mask_from_scores(nudged, zn, tau, zmax), mask)
+
+
+def test_partitioned_rejects_uneven_head_shards():
+    """The head-sharding rule of partitioning.py:46-50 needs both head axes to
+    split evenly; the check runs before anything touches a device."""
+    import torch
+
+    import orthocache_amd as oc
+
+    q = torch.zeros(1, 4, 64)
+    kv = torch.zeros(512, 2, 64)
+    m = torch.ones(1, 2, dtype=torch.bool)
+    with pytest.raises(ValueError, match="split evenly"):
+        oc.orthocache_attention_partitioned(q, kv, kv, m, num_shards=3)
+    with pytest.raises(ValueError, match=">= 1"):
+        oc.orthocache_attention_partitioned(q, kv, kv, m, num_shards=0)
