@@ -400,33 +400,68 @@ __global__ __launch_bounds__(kPfMaxThreads, 2) void attend_prefill_kernel(Attend
   // workgroup can release its LDS.
   __builtin_amdgcn_s_waitcnt(0);
 
-  // Partial for this split: m and l per row, O^T unnormalised ([D][rows]
-  // per slab, so each store of a wave writes two 128-byte row runs).
+  // Partial for this split: m and l per row, O^T unnormalised.  fp32
+  // outputs take fp32 O^T ([D][rows] per slab, so each store of a wave
+  // writes two 128-byte row runs) and (m, l) in part_ml.  16-bit outputs take
+  // O^T / s as fp16 pairs of dims ([D/2][rows] words per slab: 8-byte quads
+  // made the combine slower), s = the row's largest |o| (1 when that is 0 or
+  // infinite), and one 16-byte record
+  // (m, l, s, 0) per row after the last slab: half the bytes for the combine
+  // to read, and an error of at most 2^-12 s per value before the weights
+  // (under the 2^-9 of a bf16 output and of the bf16 P that P V multiplies).
   const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
   const int64_t rows_pad = (int64_t)nqt * kPfRows;
   const int64_t slab = ((int64_t)(split * p.num_segments + seg) * p.num_kv_heads + h);
-  if (hf == 0) {
-    st4_nt(p.part_ml + (slab * rows_pad + row) * 2, m_run);
-    st4_nt(p.part_ml + (slab * rows_pad + row) * 2 + 1, l_tot);
-  }
-  float* po = p.part_o + slab * D * rows_pad + row;
-#pragma unroll
-  for (int dt = 0; dt < DTN; ++dt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int d = dt * 32 + 8 * (i >> 2) + 4 * hf + (i & 3);
-      st4_nt(po + (int64_t)d * rows_pad, o[dt][i]);
+  if (p.out_dtype == kF32) {
+    if (hf == 0) {
+      st4_nt(p.part_ml + (slab * rows_pad + row) * 2, m_run);
+      st4_nt(p.part_ml + (slab * rows_pad + row) * 2 + 1, l_tot);
     }
+    float* po = p.part_o + slab * D * rows_pad + row;
+#pragma unroll
+    for (int dt = 0; dt < DTN; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int d = dt * 32 + 8 * (i >> 2) + 4 * hf + (i & 3);
+        st4_nt(po + (int64_t)d * rows_pad, o[dt][i]);
+      }
+  } else {
+    float mx = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DTN; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(o[dt][i]));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float sc = (mx > 0.f && mx < INFINITY) ? mx : 1.f;
+    const float inv = 1.f / sc;
+    const int64_t nslab = (int64_t)p.nsplit * p.num_segments * p.num_kv_heads;
+    if (hf == 0) {
+      const float4 rec = make_float4(m_run, l_tot, sc, 0.f);
+      st16_nt(p.part_o + nslab * (D / 2) * rows_pad + (slab * rows_pad + row) * 4, rec);
+    }
+    float* pw = p.part_o + slab * (D / 2) * rows_pad + row;
+#pragma unroll
+    for (int dt = 0; dt < DTN; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) {
+        const int d = dt * 32 + 8 * (i >> 2) + 4 * hf + (i & 3);
+        const uint32_t w = f32_to_f16_bits(o[dt][i] * inv) | (f32_to_f16_bits(o[dt][i + 1] * inv) << 16);
+        st4_nt(pw + (int64_t)(d >> 1) * rows_pad, __uint_as_float(w));
+      }
+  }
 }
 
 // Merge the splits: one workgroup per (segment, kv head, 64 query rows, 16
 // dims).  Thread t takes row t % 64 and dims 4 (t / 64) .. +3; every split's
 // (m, l) and o values are requested before any arithmetic (split indices
 // clamped, weights of missing splits zero), and the result goes through LDS
-// so output rows are written with d fastest.
+// so output rows are written with d fastest.  HALF: the partials are the
+// scaled fp16 pairs and (m, l, s) records that the attention kernel writes
+// for 16-bit outputs.
 constexpr int kCombineDims = 16;
+constexpr int kCombineDPT = kCombineDims / 4;  // dims per thread (even)
 
-template <int D>
+template <int D, bool HALF>
 __global__ __launch_bounds__(256) void prefill_combine_kernel(AttendParams p) {
   constexpr int NS = kPrefillMaxSplit;
   __shared__ float s_o[64 * (kCombineDims + 1)];
@@ -434,45 +469,63 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(AttendParams p) {
   const int64_t rows_pad = prefill_rows_pad(p);
   const int nrc = (int)(rows_pad / 64);
   constexpr int ndc = D / kCombineDims;
+  // XCD-aware order (workgroups go round-robin over the 8 XCDs): the ndc
+  // workgroups of a row chunk, which read the same (m, l) records, take
+  // consecutive slots on one XCD and share its L2.
   int id = blockIdx.x;
+  if ((gridDim.x & 7) == 0) id = (id & 7) * (int)(gridDim.x >> 3) + (id >> 3);
   const int dc = id % ndc; id /= ndc;
   const int rc = id % nrc; id /= nrc;
   const int h = id % p.num_kv_heads;
   const int seg = id / p.num_kv_heads;
   const int t = threadIdx.x;
   const int r = t & 63;
-  const int d0 = dc * kCombineDims + (t >> 6) * 4;
+  const int d0 = dc * kCombineDims + (t >> 6) * kCombineDPT;
   const int64_t row = (int64_t)rc * 64 + r;
   const int ns = p.nsplit;
   const int64_t slab_stride = (int64_t)p.num_segments * p.num_kv_heads;
   const int64_t slab0 = (int64_t)seg * p.num_kv_heads + h;
 
-  float mv[NS], lv[NS], ov[NS][4];
+  const int64_t nslab = slab_stride * ns;
+  float mv[NS], lv[NS], ov[NS][kCombineDPT];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     const int64_t slab = slab0 + (int64_t)min(s, ns - 1) * slab_stride;
-    const float2 ml = *reinterpret_cast<const float2*>(p.part_ml + (slab * rows_pad + row) * 2);
-    mv[s] = ml.x;
-    lv[s] = ml.y;
+    if constexpr (HALF) {
+      const float4 rec = reinterpret_cast<const float4*>(p.part_o + nslab * (D / 2) * rows_pad)[slab * rows_pad + row];
+      mv[s] = rec.x;
+      lv[s] = rec.y;
+      const float sc = rec.z;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) ov[s][j] = p.part_o[(slab * D + d0 + j) * rows_pad + row];
+      for (int j = 0; j < kCombineDPT / 2; ++j) {
+        const uint32_t w = __float_as_uint(p.part_o[(slab * (D / 2) + (d0 >> 1) + j) * rows_pad + row]);
+        ov[s][2 * j] = f16_bits_to_f32(w) * sc;
+        ov[s][2 * j + 1] = f16_bits_to_f32(w >> 16) * sc;
+      }
+    } else {
+      const float2 ml = *reinterpret_cast<const float2*>(p.part_ml + (slab * rows_pad + row) * 2);
+      mv[s] = ml.x;
+      lv[s] = ml.y;
+#pragma unroll
+      for (int j = 0; j < kCombineDPT; ++j) ov[s][j] = p.part_o[(slab * D + d0 + j) * rows_pad + row];
+    }
   }
   float mm = -INFINITY;
 #pragma unroll
   for (int s = 0; s < NS; ++s) mm = fmaxf(mm, s < ns ? mv[s] : -INFINITY);
-  float ll = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float ll = 0.f, acc[kCombineDPT] = {};
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     const float w = (s >= ns || mv[s] == -INFINITY) ? 0.f : exp2f(mv[s] - mm);
     if (w != 0.f) {
       ll = fmaf(lv[s], w, ll);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] = fmaf(ov[s][j], w, acc[j]);
+      for (int j = 0; j < kCombineDPT; ++j) acc[j] = fmaf(ov[s][j], w, acc[j]);
     }
   }
   const float inv = ll > 0.f ? 1.f / ll : 0.f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) s_o[r * (kCombineDims + 1) + (t >> 6) * 4 + j] = acc[j] * inv;
+  for (int j = 0; j < kCombineDPT; ++j) s_o[r * (kCombineDims + 1) + (t >> 6) * kCombineDPT + j] = acc[j] * inv;
   __syncthreads();
   for (int e = t; e < 64 * kCombineDims; e += 256) {
     const int rr = e / kCombineDims, dd = e - rr * kCombineDims;
@@ -496,7 +549,13 @@ static hipError_t launch_prefill_t(const AttendParams& p, hipStream_t s) {
     if (e != hipSuccess) return e;
   }
   const int64_t cgrid = (int64_t)p.num_segments * p.num_kv_heads * (prefill_rows_pad(p) / 64) * (D / kCombineDims);
-  if (cgrid > 0) hipLaunchKernelGGL((prefill_combine_kernel<D>), dim3((unsigned)cgrid), dim3(256), 0, s, p);
+  if (cgrid > 0) {
+    if (p.out_dtype == kF32) {
+      hipLaunchKernelGGL((prefill_combine_kernel<D, false>), dim3((unsigned)cgrid), dim3(256), 0, s, p);
+    } else {
+      hipLaunchKernelGGL((prefill_combine_kernel<D, true>), dim3((unsigned)cgrid), dim3(256), 0, s, p);
+    }
+  }
   return hipGetLastError();
 }
 

@@ -73,6 +73,30 @@ def test_unified_vs_oracle(dev, sq, hq, hkv, d, dtype, nb):
     close(np32(out16), ref, 1e-2)
 
 
+def test_half_partials_beyond_fp16_range(dev):
+    """16-bit outputs merge the splits from fp16 partials scaled by each row's
+    largest |o|: value columns near 4e4 (their unnormalised sums far beyond
+    fp16's 65504) beside columns near 1 stay within the bf16 tolerance of the
+    output scale, and the bf16 output agrees with the fp32-partial path."""
+    from orthocache_amd import _ops
+
+    nb, hkv = 12, 2
+    q, k, v = make(dev, nb, 256, 2, hkv, 128, torch.bfloat16, seed=41)
+    v = v.float()
+    v[..., :64] *= 4e4
+    v = v.to(torch.bfloat16)
+    mask = torch.ones(nb, dtype=torch.bool, device=dev)
+    c = compact(dev, mask, hkv)
+    plan = _ops.attend_plan(q, k, v, c.indices, c.num_active)
+    assert plan[0] == "prefill_mfma" and plan[1] > 1
+    out16 = _ops.attend(q, k, v, c.indices, c.num_active)
+    out32 = _ops.attend(q, k, v, c.indices, c.num_active, out_dtype=torch.float32)
+    assert torch.isfinite(out16.float()).all()
+    ref = O.attention_active_blocks(np32(q), np32(k), np32(v), range(nb))
+    close(np32(out16), ref, 1e-2)
+    close(np32(out16), np32(out32), 4e-3)
+
+
 @pytest.mark.parametrize("ntiles", [1, 2, 3, 5, 7])
 def test_short_tile_ranges(dev, ntiles):
     # 64-token blocks are one key tile each, and this shape gets a single
