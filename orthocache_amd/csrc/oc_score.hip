@@ -66,50 +66,67 @@ __device__ __forceinline__ int find_segment(const int* s_cu, int num_segments, i
 // head) 363 us against 377 us.
 // The other bf16 logits variants are held to at least two.  (Some fp16
 // logits variants need more than 256 VGPRs as scheduled and would spill under
-// a floor; they keep the compiler's choice.)
-template <int DT, int LPR, int QDT, int NQL>
+// a floor; they keep the compiler's choice.)  LPR counts the lanes of a tile
+// row, LPR / HPT those of one head.
+template <int DT, int LPR, int QDT, int NQL, int HPT>
 constexpr int score_min_waves() {
-  return (DT != kF32 && QDT == DT && ((NQL == 2 && LPR == 32) || (NQL == 4 && LPR == 16 && DT == kBF16)))
+  return (DT != kF32 && QDT == DT &&
+          ((NQL == 2 && LPR == 32 && HPT == 1) || (NQL == 4 && LPR / HPT == 16 && DT == kBF16)))
              ? 3
              : ((NQL > 0 && DT == kBF16) ? 2 : 1);
 }
 
-template <int DT, int LPR, int QDT, int NQL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(score_min_waves<DT, LPR, QDT, NQL>())))
+template <int DT, int LPR, int QDT, int NQL, int HPT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(score_min_waves<DT, LPR, QDT, NQL, HPT>())))
 void score_kernel(ScoreParams p) {
   using E = Elt<DT>;
   using EQ = Elt<QDT>;
   constexpr int VEC = E::VEC;
-  constexpr int D = LPR * VEC;
+  constexpr int DW = LPR * VEC;   // columns of a tile row: HPT heads side by side
+  constexpr int D = DW / HPT;     // head_dim
+  constexpr int LPH = LPR / HPT;  // lanes per head within a row
   constexpr int NSLOT = 256 / LPR;
   constexpr int NLO = 64 / NSLOT;
   static_assert(NLO >= 2 && (NLO % 2) == 0, "unsupported lane layout");
+  static_assert(HPT == 1 || HPT == 2, "one or two kv heads per tile");
   constexpr int ESZ = (DT == kF32) ? 4 : 2;
   constexpr int QSZ = (QDT == kF32) ? 4 : 2;
 
-  constexpr int NI = (D + 255) / 256;  // head_dim columns per thread in the epilogue
-  __shared__ float s_mean[NSLOT * D];
-  __shared__ float s_m2[NSLOT * D];
+  constexpr int NI = (DW + 255) / 256;  // tile columns per thread in the epilogue
+  __shared__ float s_mean[NSLOT * DW];
+  __shared__ float s_m2[NSLOT * DW];
   __shared__ float s_red[64];
   __shared__ int s_cu[kMaxSegLds + 1];
-  __shared__ __attribute__((aligned(16))) float s_lg[NQL > 0 ? kBlock * NQL : 4];
+  __shared__ __attribute__((aligned(16))) float s_lg[NQL > 0 ? HPT * kBlock * NQL : 4];
 
-  const int tile = blockIdx.x;
+  // Tile = (block gb, kv heads h0 .. h0 + HPT - 1); its per-head outputs are
+  // items tile0 + hh, hh < HPT.
   const int H = p.num_kv_heads;
-  const int gb = tile / H;
-  const int h = tile - gb * H;
+  const int bid = blockIdx.x;
+  const int gb = bid / (H / HPT);
+  const int h0 = (bid - gb * (H / HPT)) * HPT;
+  const int64_t tile0 = HPT == 1 ? (int64_t)bid : (int64_t)gb * H + h0;
   const int t = threadIdx.x;
   const int cc = t % LPR;
   const int slot = t / LPR;
+  const int hh = HPT == 1 ? 0 : cc / LPH;              // the lane's head within the tile
+  const int cw = HPT == 1 ? cc * VEC : (cc % LPH) * VEC;  // its first column within that head
 
   const int64_t row_bytes = p.k_tok_stride * ESZ;
   const int64_t stride64 = 64 * row_bytes;
   // Paged caches: the block's keys live in physical page pages[gb].
   const int64_t page = page_of(p.pages, p.num_pages, gb);
   const char* tbase = reinterpret_cast<const char*>(p.k) +
-                      (page * kBlock * p.k_tok_stride + (int64_t)h * p.k_head_stride) * ESZ;
+                      (page * kBlock * p.k_tok_stride + (int64_t)h0 * p.k_head_stride) * ESZ;
   // Lane offset of row l within the 64-row group: l * row_bytes + column bytes.
-  auto lane_off = [&](int l) -> uint32_t { return (uint32_t)(l * (uint32_t)row_bytes) + (uint32_t)(cc * VEC * ESZ); };
+  const uint32_t col_off =
+      HPT == 1 ? (uint32_t)(cc * VEC * ESZ) : (uint32_t)(((int64_t)hh * p.k_head_stride + cw) * ESZ);
+  auto lane_off = [&](int l) -> uint32_t { return (uint32_t)(l * (uint32_t)row_bytes) + col_off; };
+  // Query element offset of tile column dcol (head h0 + dcol / D, dim dcol % D).
+  auto qcol_off = [&](int dcol) -> int64_t {
+    if constexpr (HPT == 1) return dcol;
+    return (int64_t)(dcol / D) * p.group * p.q_head_stride + dcol % D;
+  };
 
   // Query-aware bound inputs, requested before the key stream so their
   // latency overlaps it: the segment table (ragged batches) goes to LDS, the
@@ -128,9 +145,9 @@ void score_kernel(ScoreParams p) {
     for (int u = 0; u < 4; ++u) {
       const int qi = min(u, nq - 1);
       const int st = qi / p.group, g = qi - st * p.group;
-      const int64_t qoff = (int64_t)st * p.q_tok_stride + (int64_t)(h * p.group + g) * p.q_head_stride;
+      const int64_t qoff = (int64_t)st * p.q_tok_stride + (int64_t)(h0 * p.group + g) * p.q_head_stride;
 #pragma unroll
-      for (int i = 0; i < NI; ++i) qpre[u][i] = EQ::load1(p.q, qoff + min(t + 256 * i, D - 1));
+      for (int i = 0; i < NI; ++i) qpre[u][i] = EQ::load1(p.q, qoff + qcol_off(min(t + 256 * i, DW - 1)));
     }
   }
 
@@ -190,22 +207,24 @@ void score_kernel(ScoreParams p) {
   // Sum each row's partial dots over its LPR lanes, then stage them (packed
   // dot products are scaled once, after the sum).
   auto reduce_store = [&](auto& part, int l) {
-    constexpr int V = NQL > 0 ? 8 * NQL : LPR;  // (unused without logits)
-    Butterfly<V, V, LPR / 2, LPR>::run(part, cc);
+    constexpr int V = NQL > 0 ? 8 * NQL : LPH;  // (unused without logits)
+    Butterfly<V, V, LPH / 2, LPH>::run(part, cc);
     const float sc = DOT2 ? p.logit_scale : 1.f;
-    if constexpr (V >= LPR) {
-      constexpr int PER_LANE = V / LPR;
+    float* lg = s_lg + (HPT > 1 ? hh * kBlock * NQL : 0);
+    const int ch = HPT == 1 ? cc : cc % LPH;
+    if constexpr (V >= LPH) {
+      constexpr int PER_LANE = V / LPH;
 #pragma unroll
       for (int u = 0; u < PER_LANE; ++u) {
-        const int idx = cc * PER_LANE + u;
-        s_lg[(64 * (idx / NQL) + l) * NQL + idx % NQL] = part[u] * sc;
+        const int idx = ch * PER_LANE + u;
+        lg[(64 * (idx / NQL) + l) * NQL + idx % NQL] = part[u] * sc;
       }
     } else {
-      // REP = LPR / V lanes hold each complete sum; all of them store it
+      // REP = LPH / V lanes hold each complete sum; all of them store it
       // (same address, same value), which keeps the loop free of branches.
-      constexpr int REP = LPR / V;
-      const int idx = cc / REP;
-      s_lg[(64 * (idx / NQL) + l) * NQL + idx % NQL] = part[0] * sc;
+      constexpr int REP = LPH / V;
+      const int idx = ch / REP;
+      lg[(64 * (idx / NQL) + l) * NQL + idx % NQL] = part[0] * sc;
     }
   };
 
@@ -270,7 +289,8 @@ void score_kernel(ScoreParams p) {
       const int st = qc / p.group, gg = qc - st * p.group;
       const char* qp = reinterpret_cast<const char*>(p.q) +
                        ((int64_t)seg * p.q_seg_stride + (int64_t)st * p.q_tok_stride +
-                        (int64_t)(h * p.group + gg) * p.q_head_stride + (int64_t)cc * VEC) * QSZ;
+                        (int64_t)((h0 + hh) * p.group + gg) * p.q_head_stride +
+                        (HPT == 1 ? (int64_t)cc * VEC : (int64_t)cw)) * QSZ;
       if constexpr (DOT2) {
         const uint4 w = ld16(qp);
 #pragma unroll
@@ -304,57 +324,77 @@ void score_kernel(ScoreParams p) {
     // Clamp rounding below zero without dropping NaN (fmaxf would).
     const float m2_raw = ssq[c] - ssum[c] * ssum[c] * (1.f / NLO);
     const float m2_t = m2_raw < 0.f ? 0.f : m2_raw;
-    s_mean[slot * D + cc * VEC + c] = mean_t;
-    s_m2[slot * D + cc * VEC + c] = m2_t;
+    s_mean[slot * DW + cc * VEC + c] = mean_t;
+    s_m2[slot * DW + cc * VEC + c] = m2_t;
   }
   __syncthreads();
 
   if constexpr (NQL > 0) {
-    // The tile's logits: 512 x NQL fp32, contiguous, 16 bytes per thread.
-    float* dst = p.logits + (int64_t)tile * kBlock * NQL;
+    // The tile's logits: HPT x 512 x NQL fp32, contiguous, 16 bytes per thread.
+    float* dst = p.logits + tile0 * kBlock * NQL;
 #pragma unroll
-    for (int i = 4 * t; i < kBlock * NQL; i += 4 * 256)
+    for (int i = 4 * t; i < HPT * kBlock * NQL; i += 4 * 256)
       st16_nt(dst + i, *reinterpret_cast<const float4*>(s_lg + i));
   }
 
   // Per column: merge the NSLOT partial (mean, M2) pairs (equal counts NLO).
-  float elow = 0.f;
+  // Column d of the tile row is dim d % D of head h0 + d / D; the dc rows of
+  // the tile's heads are adjacent, so column d goes to dc[tile0 * D + d].
+  float elow[HPT];
+#pragma unroll
+  for (int k = 0; k < HPT; ++k) elow[k] = 0.f;
   float kbar_r[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int d = t + 256 * i;
     kbar_r[i] = 0.f;
-    if (d < D) {
+    if (d < DW) {
       float m = 0.f;
 #pragma unroll
-      for (int s = 0; s < NSLOT; ++s) m += s_mean[s * D + d];
+      for (int s = 0; s < NSLOT; ++s) m += s_mean[s * DW + d];
       m *= (1.f / NSLOT);
       float m2 = 0.f;
 #pragma unroll
       for (int s = 0; s < NSLOT; ++s) {
-        const float dm = s_mean[s * D + d] - m;
-        m2 += s_m2[s * D + d] + (float)NLO * dm * dm;
+        const float dm = s_mean[s * DW + d] - m;
+        m2 += s_m2[s * DW + d] + (float)NLO * dm * dm;
       }
-      elow += m2;
+      if constexpr (HPT == 1) {
+        elow[0] += m2;
+      } else {
+#pragma unroll
+        for (int k = 0; k < HPT; ++k) elow[k] += (d / D == k) ? m2 : 0.f;
+      }
       const float dcv = (64.f * m) / kSqrt512;  // sum over l of y0, over sqrt(512)
-      if (p.dc) p.dc[(int64_t)tile * D + d] = dcv;
+      if (p.dc) p.dc[tile0 * D + d] = dcv;
       kbar_r[i] = dcv / kSqrt512;                // spectral_energy.py:166
     }
   }
 
-  float tot[3] = {hi, mid, elow};
-  block_sum<3>(tot, s_red);
-  const float e_high = 0.5f * tot[0];
-  const float e_mid = 0.125f * tot[1];
-  const float e_low = 0.125f * tot[2];
-  const float e_ac = e_low + e_mid + e_high;
-  const float zeta = e_high / (e_low + 1e-6f);  // spectral_energy.py:138
-  if (t == 0) {
-    if (p.e_low) p.e_low[tile] = e_low;
-    if (p.e_mid) p.e_mid[tile] = e_mid;
-    if (p.e_high) p.e_high[tile] = e_high;
-    if (p.e_ac) p.e_ac[tile] = e_ac;
-    if (p.zeta) p.zeta[tile] = zeta;
+  // Band totals per head: a lane's columns all belong to head hh.
+  float tot[3 * HPT];
+#pragma unroll
+  for (int k = 0; k < HPT; ++k) {
+    tot[3 * k] = (HPT == 1 || hh == k) ? hi : 0.f;
+    tot[3 * k + 1] = (HPT == 1 || hh == k) ? mid : 0.f;
+    tot[3 * k + 2] = elow[k];
+  }
+  block_sum<3 * HPT>(tot, s_red);
+  float e_ac[HPT], zeta[HPT];
+#pragma unroll
+  for (int k = 0; k < HPT; ++k) {
+    const float e_high = 0.5f * tot[3 * k];
+    const float e_mid = 0.125f * tot[3 * k + 1];
+    const float e_low = 0.125f * tot[3 * k + 2];
+    e_ac[k] = e_low + e_mid + e_high;
+    zeta[k] = e_high / (e_low + 1e-6f);  // spectral_energy.py:138
+    if (t == 0) {
+      if (p.e_low) p.e_low[tile0 + k] = e_low;
+      if (p.e_mid) p.e_mid[tile0 + k] = e_mid;
+      if (p.e_high) p.e_high[tile0 + k] = e_high;
+      if (p.e_ac) p.e_ac[tile0 + k] = e_ac[k];
+      if (p.zeta) p.zeta[tile0 + k] = zeta[k];
+    }
   }
 
   // Inline query-aware bound: tau_j = q.kbar/sqrt(d) + ||q|| sqrt(E_AC)/sqrt(d),
@@ -366,8 +406,12 @@ void score_kernel(ScoreParams p) {
   }
   if (want_bound) {
     const float sqrt_d = sqrtf((float)D);
-    const float sqrt_eac = sqrtf(e_ac);
-    float best = -INFINITY;
+    float best[HPT], sqrt_eac[HPT];
+#pragma unroll
+    for (int k = 0; k < HPT; ++k) {
+      best[k] = -INFINITY;
+      sqrt_eac[k] = sqrtf(e_ac[k]);
+    }
     for (int q0 = 0; q0 < nq; q0 += 4) {
       float qv[4][NI];
       if (prefetch && q0 == 0) {
@@ -381,42 +425,52 @@ void score_kernel(ScoreParams p) {
           const int qi = min(q0 + u, nq - 1);
           const int st = qi / p.group, g = qi - st * p.group;
           const int64_t qoff = (int64_t)seg * p.q_seg_stride + (int64_t)st * p.q_tok_stride +
-                               (int64_t)(h * p.group + g) * p.q_head_stride;
+                               (int64_t)(h0 * p.group + g) * p.q_head_stride;
 #pragma unroll
-          for (int i = 0; i < NI; ++i) qv[u][i] = EQ::load1(p.q, qoff + min(t + 256 * i, D - 1));
+          for (int i = 0; i < NI; ++i) qv[u][i] = EQ::load1(p.q, qoff + qcol_off(min(t + 256 * i, DW - 1)));
         }
       }
-      float part[8];
+      // Per query and head: q.kbar and |q|^2 over the head's columns.
+      float part[8 * HPT];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        float a = 0.f, b = 0.f;
+      for (int k = 0; k < HPT; ++k)
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          const float v = (t + 256 * i < D) ? qv[u][i] : 0.f;
-          a = fmaf(v, kbar_r[i], a);
-          b = fmaf(v, v, b);
+        for (int u = 0; u < 4; ++u) {
+          float a = 0.f, b = 0.f;
+#pragma unroll
+          for (int i = 0; i < NI; ++i) {
+            const int d = t + 256 * i;
+            const float v = (d < DW && (HPT == 1 || d / D == k)) ? qv[u][i] : 0.f;
+            a = fmaf(v, kbar_r[i], a);
+            b = fmaf(v, v, b);
+          }
+          part[8 * k + 2 * u] = a;
+          part[8 * k + 2 * u + 1] = b;
         }
-        part[2 * u] = a;
-        part[2 * u + 1] = b;
-      }
-      block_sum<8>(part, s_red);
+      block_sum<8 * HPT>(part, s_red);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if (q0 + u < nq) {
-          const float align = part[2 * u] / sqrt_d;
-          const float resid = (sqrtf(part[2 * u + 1]) * sqrt_eac) / sqrt_d;
-          best = nanmax(align + resid, best);
+      for (int k = 0; k < HPT; ++k) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (q0 + u < nq) {
+            const float align = part[8 * k + 2 * u] / sqrt_d;
+            const float resid = (sqrtf(part[8 * k + 2 * u + 1]) * sqrt_eac[k]) / sqrt_d;
+            best[k] = nanmax(align + resid, best[k]);
+          }
         }
       }
     }
     if (t == 0) {
-      p.tau_max[tile] = best;
-      // The two-gate mask of this tile (compute_multiband_mask,
-      // spectral_energy.py:199-234), from the same fp32 scores.
-      if (p.gate.keep) {
-        const uint8_t k = gate_keep(p.gate, seg, best, zeta);
-        p.gate.keep[tile] = k;
-        if (p.gate.mask_out) p.gate.mask_out[tile] = k;
+#pragma unroll
+      for (int k = 0; k < HPT; ++k) {
+        p.tau_max[tile0 + k] = best[k];
+        // The two-gate mask of this tile (compute_multiband_mask,
+        // spectral_energy.py:199-234), from the same fp32 scores.
+        if (p.gate.keep) {
+          const uint8_t kf = gate_keep(p.gate, seg, best[k], zeta[k]);
+          p.gate.keep[tile0 + k] = kf;
+          if (p.gate.mask_out) p.gate.mask_out[tile0 + k] = kf;
+        }
       }
     }
   }
@@ -665,40 +719,46 @@ __global__ __launch_bounds__(256) void block_energy_kernel(EnergyParams p) {
 // ---------------------------------------------------------------- launchers
 namespace oc {
 
-template <int DT, int LPR, int QDT>
+template <int DT, int LPR, int QDT, int HPT>
 static hipError_t launch_score_q(const ScoreParams& p, hipStream_t s) {
-  const int tiles = p.total_blocks * p.num_kv_heads;
+  const int tiles = p.total_blocks * (p.num_kv_heads / HPT);
   if (!p.logits) {
-    hipLaunchKernelGGL((score_kernel<DT, LPR, QDT, 0>), dim3(tiles), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((score_kernel<DT, LPR, QDT, 0, HPT>), dim3(tiles), dim3(256), 0, s, p);
     return hipGetLastError();
   }
-  // Logits: lanes per row of the attention's value loads (LPR <= 64).
-  if constexpr (LPR <= 64) {
+  // Logits: lanes per head row of the attention's value loads (<= 64).
+  if constexpr (LPR / HPT <= 64) {
     switch (logits_nq_pad(p.sq * p.group)) {
-      case 1: hipLaunchKernelGGL((score_kernel<DT, LPR, QDT, 1>), dim3(tiles), dim3(256), 0, s, p); break;
-      case 2: hipLaunchKernelGGL((score_kernel<DT, LPR, QDT, 2>), dim3(tiles), dim3(256), 0, s, p); break;
-      default: hipLaunchKernelGGL((score_kernel<DT, LPR, QDT, 4>), dim3(tiles), dim3(256), 0, s, p); break;
+      case 1: hipLaunchKernelGGL((score_kernel<DT, LPR, QDT, 1, HPT>), dim3(tiles), dim3(256), 0, s, p); break;
+      case 2: hipLaunchKernelGGL((score_kernel<DT, LPR, QDT, 2, HPT>), dim3(tiles), dim3(256), 0, s, p); break;
+      default: hipLaunchKernelGGL((score_kernel<DT, LPR, QDT, 4, HPT>), dim3(tiles), dim3(256), 0, s, p); break;
     }
     return hipGetLastError();
   }
   return hipErrorInvalidValue;
 }
 
-template <int DT, int LPR>
+template <int DT, int LPR, int HPT = 1>
 static hipError_t launch_score_t(const ScoreParams& p, hipStream_t s) {
   // Without queries the query type is irrelevant: use the key type.
   const int qdt = p.q ? p.q_dtype : DT;
-  if (qdt == DT) return launch_score_q<DT, LPR, DT>(p, s);
-  if (qdt == kF32) return launch_score_q<DT, LPR, kF32>(p, s);
+  if (qdt == DT) return launch_score_q<DT, LPR, DT, HPT>(p, s);
+  if (qdt == kF32) return launch_score_q<DT, LPR, kF32, HPT>(p, s);
   return hipErrorInvalidValue;
 }
 
+// Heads with 128- or 256-byte rows (8 or 16 lanes of 16 bytes: bf16/fp16
+// head_dim 64 or 128, fp32 32 or 64) are scored two per tile when the head
+// count is even, so a tile row is twice as long; head_dim 128 then reads as
+// head_dim 256 does: C3's scoring pass with logits 208 -> 190 us, without 176 ->
+// 165 us at the same bytes (the per-tile merge, reductions and bound are
+// shared by twice the keys).
 template <int DT>
 static hipError_t launch_score_dt(const ScoreParams& p, hipStream_t s) {
   const int lpr = p.head_dim / Elt<DT>::VEC;
   switch (lpr) {
-    case 8: return launch_score_t<DT, 8>(p, s);
-    case 16: return launch_score_t<DT, 16>(p, s);
+    case 8: return p.num_kv_heads % 2 == 0 ? launch_score_t<DT, 16, 2>(p, s) : launch_score_t<DT, 8>(p, s);
+    case 16: return p.num_kv_heads % 2 == 0 ? launch_score_t<DT, 32, 2>(p, s) : launch_score_t<DT, 16>(p, s);
     case 32: return launch_score_t<DT, 32>(p, s);
     case 64: return launch_score_t<DT, 64>(p, s);
     case 128: return launch_score_t<DT, 128>(p, s);
