@@ -403,12 +403,12 @@ __global__ __launch_bounds__(kPfMaxThreads, 2) void attend_prefill_kernel(Attend
   // Partial for this split: m and l per row, O^T unnormalised.  fp32
   // outputs take fp32 O^T ([D][rows] per slab, so each store of a wave
   // writes two 128-byte row runs) and (m, l) in part_ml.  16-bit outputs take
-  // O^T / s as fp16 pairs of dims ([D/2][rows] words per slab: 8-byte quads
-  // made the combine slower), s = the row's largest |o| (1 when that is 0 or
-  // infinite), and one 16-byte record
-  // (m, l, s, 0) per row after the last slab: half the bytes for the combine
-  // to read, and an error of at most 2^-12 s per value before the weights
-  // (under the 2^-9 of a bf16 output and of the bf16 P that P V multiplies).
+  // O / s in fp16, row-major ([rows][D] per slab), s = the row's largest |o|
+  // (1 when that is 0 or infinite), and one 16-byte record (m, l, s, 0) per
+  // row after the last slab: half the bytes for the combine to read, in
+  // whole 16-byte pieces of a row, and an error of at most 2^-12 s per value
+  // before the weights (under the 2^-9 of a bf16 output and of the bf16 P
+  // that P V multiplies).
   const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
   const int64_t rows_pad = (int64_t)nqt * kPfRows;
   const int64_t slab = ((int64_t)(split * p.num_segments + seg) * p.num_kv_heads + h);
@@ -439,15 +439,34 @@ __global__ __launch_bounds__(kPfMaxThreads, 2) void attend_prefill_kernel(Attend
       const float4 rec = make_float4(m_run, l_tot, sc, 0.f);
       st16_nt(p.part_o + nslab * (D / 2) * rows_pad + (slab * rows_pad + row) * 4, rec);
     }
-    float* pw = p.part_o + slab * (D / 2) * rows_pad + row;
+    // Stage the wave's 32 rows in LDS (the tiles' buffers are free once every
+    // wave is past its last step), then write whole rows with 16-byte stores.
+    // Chunk c (16 bytes) of row r sits at chunk c ^ (r % CPR) of its LDS row.
+    typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
+    constexpr int CPR = 2 * D / 16;
+    static_assert(2 * 32 * 2 * D == TBYTES && kPfThreads / kWave <= 8, "two waves' rows per tile buffer, four buffers");
+    __syncthreads();
+    const int bsel = wave >> 1;
+    char* sb = bsel == 0 ? s_k0 : (bsel == 1 ? s_k1 : (bsel == 2 ? s_k2 : s_v0));
+    char* stg = sb + (wave & 1) * 32 * (2 * D);
 #pragma unroll
     for (int dt = 0; dt < DTN; ++dt)
 #pragma unroll
-      for (int i = 0; i < 16; i += 2) {
-        const int d = dt * 32 + 8 * (i >> 2) + 4 * hf + (i & 3);
-        const uint32_t w = f32_to_f16_bits(o[dt][i] * inv) | (f32_to_f16_bits(o[dt][i + 1] * inv) << 16);
-        st4_nt(pw + (int64_t)(d >> 1) * rows_pad, __uint_as_float(w));
+      for (int i = 0; i < 16; i += 4) {
+        const int c16 = dt * 4 + (i >> 2);
+        u32x2v w;
+        w.x = f32_to_f16_bits(o[dt][i] * inv) | (f32_to_f16_bits(o[dt][i + 1] * inv) << 16);
+        w.y = f32_to_f16_bits(o[dt][i + 2] * inv) | (f32_to_f16_bits(o[dt][i + 3] * inv) << 16);
+        *reinterpret_cast<u32x2v*>(stg + q32 * (2 * D) + ((c16 ^ (q32 & (CPR - 1))) * 16) + 8 * hf) = w;
       }
+    u32x4_t* pw = reinterpret_cast<u32x4_t*>(p.part_o) + (slab * rows_pad + (row - q32)) * CPR;
+#pragma unroll
+    for (int k = 0; k < 32 * CPR / kWave; ++k) {
+      const int c = lane + kWave * k;
+      const int r = c / CPR, e = c % CPR;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(stg + r * (2 * D) + ((e ^ (r & (CPR - 1))) * 16));
+      __builtin_nontemporal_store(v, pw + c);
+    }
   }
 }
 
@@ -455,13 +474,11 @@ __global__ __launch_bounds__(kPfMaxThreads, 2) void attend_prefill_kernel(Attend
 // dims).  Thread t takes row t % 64 and dims 4 (t / 64) .. +3; every split's
 // (m, l) and o values are requested before any arithmetic (split indices
 // clamped, weights of missing splits zero), and the result goes through LDS
-// so output rows are written with d fastest.  HALF: the partials are the
-// scaled fp16 pairs and (m, l, s) records that the attention kernel writes
-// for 16-bit outputs.
+// so output rows are written with d fastest.  fp32 outputs (fp32 partials).
 constexpr int kCombineDims = 16;
-constexpr int kCombineDPT = kCombineDims / 4;  // dims per thread (even)
+constexpr int kCombineDPT = kCombineDims / 4;  // dims per thread
 
-template <int D, bool HALF>
+template <int D>
 __global__ __launch_bounds__(256) void prefill_combine_kernel(AttendParams p) {
   constexpr int NS = kPrefillMaxSplit;
   __shared__ float s_o[64 * (kCombineDims + 1)];
@@ -470,7 +487,7 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(AttendParams p) {
   const int nrc = (int)(rows_pad / 64);
   constexpr int ndc = D / kCombineDims;
   // XCD-aware order (workgroups go round-robin over the 8 XCDs): the ndc
-  // workgroups of a row chunk, which read the same (m, l) records, take
+  // workgroups of a row chunk, which read the same (m, l) values, take
   // consecutive slots on one XCD and share its L2.
   int id = blockIdx.x;
   if ((gridDim.x & 7) == 0) id = (id & 7) * (int)(gridDim.x >> 3) + (id >> 3);
@@ -486,29 +503,15 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(AttendParams p) {
   const int64_t slab_stride = (int64_t)p.num_segments * p.num_kv_heads;
   const int64_t slab0 = (int64_t)seg * p.num_kv_heads + h;
 
-  const int64_t nslab = slab_stride * ns;
   float mv[NS], lv[NS], ov[NS][kCombineDPT];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     const int64_t slab = slab0 + (int64_t)min(s, ns - 1) * slab_stride;
-    if constexpr (HALF) {
-      const float4 rec = reinterpret_cast<const float4*>(p.part_o + nslab * (D / 2) * rows_pad)[slab * rows_pad + row];
-      mv[s] = rec.x;
-      lv[s] = rec.y;
-      const float sc = rec.z;
+    const float2 ml = *reinterpret_cast<const float2*>(p.part_ml + (slab * rows_pad + row) * 2);
+    mv[s] = ml.x;
+    lv[s] = ml.y;
 #pragma unroll
-      for (int j = 0; j < kCombineDPT / 2; ++j) {
-        const uint32_t w = __float_as_uint(p.part_o[(slab * (D / 2) + (d0 >> 1) + j) * rows_pad + row]);
-        ov[s][2 * j] = f16_bits_to_f32(w) * sc;
-        ov[s][2 * j + 1] = f16_bits_to_f32(w >> 16) * sc;
-      }
-    } else {
-      const float2 ml = *reinterpret_cast<const float2*>(p.part_ml + (slab * rows_pad + row) * 2);
-      mv[s] = ml.x;
-      lv[s] = ml.y;
-#pragma unroll
-      for (int j = 0; j < kCombineDPT; ++j) ov[s][j] = p.part_o[(slab * D + d0 + j) * rows_pad + row];
-    }
+    for (int j = 0; j < kCombineDPT; ++j) ov[s][j] = p.part_o[(slab * D + d0 + j) * rows_pad + row];
   }
   float mm = -INFINITY;
 #pragma unroll
@@ -539,6 +542,80 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(AttendParams p) {
   }
 }
 
+// Merge the splits for 16-bit outputs, from the row-major fp16 partials and
+// (m, l, s) records: thread = (row, 8 dims), D / 8 lanes per row, so every
+// split's 16-byte load of a row piece and the row's record (one address per
+// row) are coalesced, and the 8 outputs go out in one 16-byte store (scalar
+// stores when the output row is not 16-byte aligned).
+template <int D>
+__global__ __launch_bounds__(256) void prefill_combine_half_kernel(AttendParams p) {
+  constexpr int NS = kPrefillMaxSplit;
+  constexpr int LPRW = D / 8;            // lanes per row
+  constexpr int RPW = 256 / LPRW;        // rows per workgroup
+  const int nq_rows = prefill_rows(p);
+  const int64_t rows_pad = prefill_rows_pad(p);
+  const int nrc = (int)(rows_pad / RPW);
+  int id = blockIdx.x;
+  const int rc = id % nrc; id /= nrc;
+  const int h = id % p.num_kv_heads;
+  const int seg = id / p.num_kv_heads;
+  const int t = threadIdx.x;
+  const int e = t % LPRW;
+  const int64_t row = (int64_t)rc * RPW + t / LPRW;
+  const int ns = p.nsplit;
+  const int64_t slab_stride = (int64_t)p.num_segments * p.num_kv_heads;
+  const int64_t slab0 = (int64_t)seg * p.num_kv_heads + h;
+  const int64_t nslab = slab_stride * ns;
+  const float4* recs = reinterpret_cast<const float4*>(p.part_o + nslab * (D / 2) * rows_pad);
+  const u32x4_t* data = reinterpret_cast<const u32x4_t*>(p.part_o);
+  float mv[NS], lv[NS], sv[NS];
+  u32x4_t ov[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int64_t slab = slab0 + (int64_t)min(s, ns - 1) * slab_stride;
+    const float4 rec = recs[slab * rows_pad + row];
+    mv[s] = rec.x; lv[s] = rec.y; sv[s] = rec.z;
+    ov[s] = data[(slab * rows_pad + row) * (D / 8) + e];
+  }
+  float mm = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) mm = fmaxf(mm, s < ns ? mv[s] : -INFINITY);
+  float ll = 0.f, acc[8] = {};
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const float w = (s >= ns || mv[s] == -INFINITY) ? 0.f : exp2f(mv[s] - mm);
+    if (w != 0.f) {
+      ll = fmaf(lv[s], w, ll);
+      const float ws = w * sv[s];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[2 * j] = fmaf(f16_bits_to_f32(ov[s][j]), ws, acc[2 * j]);
+        acc[2 * j + 1] = fmaf(f16_bits_to_f32(ov[s][j] >> 16), ws, acc[2 * j + 1]);
+      }
+    }
+  }
+  if (row < nq_rows) {
+    const float inv = ll > 0.f ? 1.f / ll : 0.f;
+    const int st = (int)(row / p.group), g = (int)(row - (int64_t)st * p.group);
+    const int64_t o = (int64_t)seg * p.out_seg_stride + (int64_t)st * p.out_tok_stride +
+                      (int64_t)(h * p.group + g) * p.out_head_stride + 8 * e;
+    char* op = reinterpret_cast<char*>(p.out) + o * 2;
+    if ((reinterpret_cast<uintptr_t>(op) & 15) == 0) {
+      u32x4_t w;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float a = acc[2 * j] * inv, b = acc[2 * j + 1] * inv;
+        w[j] = p.out_dtype == kBF16 ? (f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16))
+                                    : (f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16));
+      }
+      *reinterpret_cast<u32x4_t*>(op) = w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) store_elt(p.out_dtype, p.out, o + j, acc[j] * inv);
+    }
+  }
+}
+
 template <int DT, int D>
 static hipError_t launch_prefill_t(const AttendParams& p, hipStream_t s) {
   const int nqt = prefill_qtiles(p);
@@ -551,9 +628,10 @@ static hipError_t launch_prefill_t(const AttendParams& p, hipStream_t s) {
   const int64_t cgrid = (int64_t)p.num_segments * p.num_kv_heads * (prefill_rows_pad(p) / 64) * (D / kCombineDims);
   if (cgrid > 0) {
     if (p.out_dtype == kF32) {
-      hipLaunchKernelGGL((prefill_combine_kernel<D, false>), dim3((unsigned)cgrid), dim3(256), 0, s, p);
+      hipLaunchKernelGGL((prefill_combine_kernel<D>), dim3((unsigned)cgrid), dim3(256), 0, s, p);
     } else {
-      hipLaunchKernelGGL((prefill_combine_kernel<D, true>), dim3((unsigned)cgrid), dim3(256), 0, s, p);
+      const int64_t hgrid = (int64_t)p.num_segments * p.num_kv_heads * (prefill_rows_pad(p) / (256 / (D / 8)));
+      hipLaunchKernelGGL((prefill_combine_half_kernel<D>), dim3((unsigned)hgrid), dim3(256), 0, s, p);
     }
   }
   return hipGetLastError();
