@@ -95,12 +95,13 @@ class TestBands:
                                           (512, torch.float32), (64, torch.bfloat16), (128, torch.bfloat16),
                                           (256, torch.bfloat16), (512, torch.bfloat16), (1024, torch.bfloat16),
                                           (128, torch.float16), (32, torch.float32)])
-    def test_all_layouts(self, dev, d, dtype):
+    @pytest.mark.parametrize("hkv", [3, 4])  # 4: heads with 128- or 256-byte rows are scored two per tile
+    def test_all_layouts(self, dev, d, dtype, hkv):
         import orthocache_amd as oc
 
-        rng = np.random.default_rng(d)
-        keys = (rng.standard_normal((1536, 3, d)) + rng.standard_normal((3, 1, 3, d)).repeat(512, 0).reshape(1536, 3, d)
-                ).astype(np.float32)
+        rng = np.random.default_rng(d + hkv)
+        keys = (rng.standard_normal((1536, hkv, d)) +
+                rng.standard_normal((3, 1, hkv, d)).repeat(512, 0).reshape(1536, hkv, d)).astype(np.float32)
         kd = to_dev(keys, dev, dtype)
         kref = np32(kd)  # the values the GPU sees
         dc, lo, mi, hi = oc.compute_spectral_bands(kd)
@@ -178,15 +179,18 @@ class TestBounds:
         ref = O.query_aware_bounds(O.fold_gqa(q, hkv), keys)
         np.testing.assert_allclose(b, ref, rtol=1e-5, atol=1e-5)
 
-    @pytest.mark.parametrize("sq,hq,hkv", [(1, 32, 16), (2, 8, 2), (64, 4, 4)])
-    def test_tau_max_inline_and_tiled(self, dev, sq, hq, hkv):
+    @pytest.mark.parametrize("sq,hq,hkv", [(1, 32, 16), (2, 8, 2), (64, 4, 4), (1, 32, 8), (3, 9, 3)])
+    @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+    def test_tau_max_inline_and_tiled(self, dev, sq, hq, hkv, dtype):
         from orthocache_amd import _ops
 
         d = 128
         rng = np.random.default_rng(sq + hq)
         q = rng.standard_normal((sq, hq, d)).astype(np.float32)
         keys = rng.standard_normal((2048, hkv, d)).astype(np.float32)
-        sc = _ops.score(to_dev(keys, dev), to_dev(q, dev))
+        kd, qd = to_dev(keys, dev, dtype), to_dev(q, dev, dtype)
+        keys, q = np32(kd), np32(qd)  # the values the GPU sees
+        sc = _ops.score(kd, qd)
         tm = np32(sc.tau_max).max(axis=0)
         ref = O.nanmax_axis0(O.query_aware_bounds(O.fold_gqa(q, hkv), keys))
         np.testing.assert_allclose(tm, ref, rtol=1e-5, atol=1e-5)
