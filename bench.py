@@ -73,6 +73,16 @@ def event_time_us(fn, reps, torch):
     return start.elapsed_time(stop) * 1000.0 / reps
 
 
+def _score_kernel_name(d: int, hkv: int, nq_pad: int) -> str:
+    """The scoring kernel instantiation the library launches for bf16 keys and
+    queries (oc_score.hip launch_score_dt): heads with 128- or 256-byte rows go
+    two per tile when the head count is even."""
+    lanes, hpt = d // 8, 1
+    if lanes in (8, 16) and hkv % 2 == 0:
+        lanes, hpt = 2 * lanes, 2
+    return f"score_kernel<bf16, {lanes}, bf16, {nq_pad}, {hpt}>"
+
+
 def _cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -366,7 +376,7 @@ def run_c4(args, torch, dev):
                    "attend_plan": list(plan)},
         "kernels_us": {k: round(v, 2) for k, v in kus.items()},
         "attend_flops": flops,
-        "roofline": {"bound": "mfma", "kernel": "attend_prefill_kernel<bf16, 128> + prefill_combine_kernel",
+        "roofline": {"bound": "mfma", "kernel": "attend_prefill_kernel<bf16, 128> + prefill_combine_half_kernel<128>",
                      "achieved": round(tflops, 1), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(tflops / peak, 4), "traffic": None},
     }
@@ -498,7 +508,7 @@ def run_c3(args, torch, dev):
              "layer_frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
              "kernels_us": {k: round(v, 2) for k, v in kus.items()},
              "roofline": {"bound": "hbm",
-                          "kernel": f"score_kernel<bf16, 16, bf16, {_ops.logits_nq_pad(nq)}> (segments)",
+                          "kernel": _score_kernel_name(wl.k.shape[-1], hkv, _ops.logits_nq_pad(nq)) + " (segments)",
                           "achieved": round(score_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": round(score_gbs / PEAK_HBM_GBS, 4), "traffic": None,
                           "algorithmic_bytes": score_bytes, "kernel_us": round(kus["score"], 2)}}
