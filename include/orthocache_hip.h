@@ -374,6 +374,30 @@ int oc_decode_layer_cached(const oc_layer_args* a, const oc_block_stats* stats, 
 #define OC_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 int oc_decode_layer_noalloc(const oc_layer_args* a, void* stream);
 
+/* ---------------------------------------------------- reference custom call
+ * The reference's own C entry point for its compacted attention, under its
+ * name and signature (notebooks/phase_d_kaggle.py:211-222, the XLA custom
+ * call orthocache_compacted_attention(void* out, const void** inputs) and its
+ * five-int32 CompactedAttentionDescriptor, same field order), so a caller
+ * bound to that symbol links against this library unchanged.  Here the
+ * buffers are device memory: inputs[0] q fp32 (seq_len_q, head_dim),
+ * inputs[1] keys and inputs[2] values fp32 (num_blocks * block_size,
+ * head_dim), inputs[3] block_mask int32 (num_blocks; nonzero = active);
+ * inputs[4] points to the descriptor in host memory; out fp32 (seq_len_q,
+ * head_dim).  Softmax attention of each query over the tokens of the active
+ * blocks only, with scale 1/sqrt(head_dim); rows are zero when no block is
+ * active.  Runs on the null stream and returns when out is written (the
+ * reference's function is synchronous); allocates its workspace per call.
+ * Supported: head_dim 32, 64, 128 or 256, any number of blocks (the
+ * reference's own function holds at most 4096), seq_len_k = num_blocks *
+ * block_size.  There is no return value, as
+ * in the reference: on an error out is left unchanged and oc_last_error()
+ * names it (it is not cleared on success). */
+typedef struct oc_compacted_attention_desc {
+  int32_t seq_len_q, seq_len_k, head_dim, block_size, num_blocks;
+} oc_compacted_attention_desc;
+void orthocache_compacted_attention(void* out, const void** inputs);
+
 #ifdef __cplusplus
 }
 #endif

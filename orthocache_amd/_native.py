@@ -99,6 +99,7 @@ EXPORTED_SYMBOLS = (
     "oc_copy_blocks", "oc_attend_workspace_size", "oc_attend", "oc_attend_plan",
     "oc_decode_layer_workspace_size", "oc_decode_layer",
     "oc_decode_layer_cached_workspace_size", "oc_decode_layer_cached", "oc_decode_layer_noalloc",
+    "orthocache_compacted_attention",
 )
 
 NOALLOC_SCRATCH_BYTES = 32 << 20  # OC_NOALLOC_SCRATCH_BYTES
@@ -144,6 +145,8 @@ def lib() -> C.CDLL:
     L.oc_decode_layer_cached_workspace_size.restype = C.c_size_t
     L.oc_decode_layer_cached.argtypes = [C.POINTER(LayerArgs), C.POINTER(BlockStats), _vp, C.c_size_t, _vp]
     L.oc_decode_layer_cached.restype = C.c_int
+    L.orthocache_compacted_attention.argtypes = [_vp, C.POINTER(_vp)]
+    L.orthocache_compacted_attention.restype = None
     _lib = L
     return L
 

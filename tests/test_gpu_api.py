@@ -11,9 +11,12 @@ the way a reference caller would and compares its result with the oracle:
   orthocache_attention_partitioned, orthocache_forward(mode='sparse'))
   against the float64 oracle over the retained tokens;
 * auto-tau (orthocache_forward(tau=None)) against the oracle's pinned
-  mean - population-std on the same fp32 scores.
+  mean - population-std on the same fp32 scores;
+* the reference's C custom-call entry point (orthocache_compacted_attention)
+  against the oracle and the reference's compiled CPU function.
 """
 
+import ctypes
 import math
 
 import numpy as np
@@ -352,3 +355,66 @@ def test_forward_auto_tau(dev):
     order, n = O.stream_compact_indices(mask)
     assert meta["blocks_retained"] == n
     close(np32(out), O.attention_active_blocks(np32(q), np32(k), np32(v), order[:n]), 1e-4)
+
+
+class _CADesc(ctypes.Structure):
+    # notebooks/phase_d_kaggle.py:211-217 (CompactedAttentionDescriptor)
+    _fields_ = [("seq_len_q", ctypes.c_int32), ("seq_len_k", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+                ("block_size", ctypes.c_int32), ("num_blocks", ctypes.c_int32)]
+
+
+def _custom_call(q, k, v, m, bs, out):
+    from orthocache_amd import _native as N
+
+    L = N.lib()
+    desc = _CADesc(q.shape[0], k.shape[0], q.shape[1], bs, m.shape[0])
+    ins = (ctypes.c_void_p * 5)(q.data_ptr(), k.data_ptr(), v.data_ptr(), m.data_ptr(), ctypes.addressof(desc))
+    L.orthocache_compacted_attention(ctypes.c_void_p(out.data_ptr()), ins)
+
+
+@pytest.mark.parametrize("sq,d,bs,nb", [(1, 128, 512, 8), (7, 64, 128, 12), (33, 256, 64, 5), (4, 32, 512, 3),
+                                        (600, 128, 256, 4), (2, 64, 64, 3000)])
+def test_reference_custom_call_entry_point(dev, sq, d, bs, nb):
+    """orthocache_compacted_attention under the reference's own signature
+    (notebooks/phase_d_kaggle.py:211-222) on device buffers: against the
+    float64 oracle and, where it is built, the reference's compiled CPU
+    function on the same inputs."""
+    from oracle import native
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(sq * 31 + nb)
+    q = torch.randn(sq, d, generator=g, device=dev) / math.sqrt(d)
+    k = torch.randn(nb * bs, d, generator=g, device=dev)
+    v = torch.randn(nb * bs, d, generator=g, device=dev)
+    rng = np.random.default_rng(nb + d)
+    m = (rng.random(nb) < 0.5).astype(np.int32) * rng.integers(1, 5, nb).astype(np.int32)  # any nonzero is active
+    m[rng.integers(nb)] = -3
+    md = torch.from_numpy(m).to(dev)
+    out = torch.full((sq, d), float("nan"), device=dev)
+    _custom_call(q, k, v, md, bs, out)
+    active = np.flatnonzero(m)
+    ref = O.attention_active_blocks(np32(q)[:, None], np32(k)[:, None], np32(v)[:, None], active, block_size=bs)[:, 0]
+    close(np32(out), ref, 1e-4)
+    if native.ref_available():
+        close(np32(out), native.ref_compacted_attention(np32(q), np32(k), np32(v), m, block_size=bs), 1e-4)
+
+
+def test_reference_custom_call_no_active_block(dev):
+    """No active block (and no block at all) gives zero rows, as the
+    reference's r_sum guard does; a descriptor whose seq_len_k is not
+    num_blocks * block_size is refused and out is left alone."""
+    from orthocache_amd import _native as N
+
+    q = torch.randn(3, 64, device=dev)
+    k = torch.randn(4 * 128, 64, device=dev)
+    v = torch.randn(4 * 128, 64, device=dev)
+    out = torch.full((3, 64), float("nan"), device=dev)
+    _custom_call(q, k, v, torch.zeros(4, dtype=torch.int32, device=dev), 128, out)
+    assert float(out.abs().sum()) == 0.0
+    out.fill_(float("nan"))
+    _custom_call(q, k[:0], v[:0], torch.zeros(0, dtype=torch.int32, device=dev), 128, out)
+    assert float(out.abs().sum()) == 0.0
+    out.fill_(float("nan"))
+    _custom_call(q, k[:300], v[:300], torch.ones(4, dtype=torch.int32, device=dev), 128, out)
+    assert torch.isnan(out).all()
+    assert b"seq_len_k" in N.lib().oc_last_error()

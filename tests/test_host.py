@@ -22,7 +22,7 @@ HEADER = os.path.join(ROOT, "include", "orthocache_hip.h")
 def _declared_symbols():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(oc_[a-z0-9_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b((?:oc|orthocache)_[a-z0-9_]+)\s*\(", text)))
 
 
 @pytest.fixture(scope="module")
@@ -324,3 +324,26 @@ def test_partitioned_rejects_uneven_head_shards():
         oc.orthocache_attention_partitioned(q, kv, kv, m, num_shards=3)
     with pytest.raises(ValueError, match=">= 1"):
         oc.orthocache_attention_partitioned(q, kv, kv, m, num_shards=0)
+
+
+def test_custom_call_rejects_bad_descriptors(lib):
+    """orthocache_compacted_attention checks its descriptor before any device
+    call: a missing descriptor, negative sizes and a key count that is not
+    num_blocks * block_size leave oc_last_error() set; no query rows is a
+    no-op."""
+
+    class Desc(C.Structure):
+        _fields_ = [("seq_len_q", C.c_int32), ("seq_len_k", C.c_int32), ("head_dim", C.c_int32),
+                    ("block_size", C.c_int32), ("num_blocks", C.c_int32)]
+
+    def call(desc):
+        ins = (C.c_void_p * 5)(16, 16, 16, 16, C.addressof(desc) if desc is not None else None)
+        lib.orthocache_compacted_attention(C.c_void_p(16), ins)
+        return lib.oc_last_error()
+
+    assert b"descriptor" in call(None)
+    assert b"num_blocks -1" in call(Desc(1, 512, 64, 512, -1))
+    assert b"seq_len_k 500" in call(Desc(1, 500, 64, 512, 1))
+    before = lib.oc_last_error()
+    call(Desc(0, 512, 64, 512, 1))
+    assert lib.oc_last_error() == before
