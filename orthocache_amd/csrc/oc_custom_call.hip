@@ -41,6 +41,8 @@ int run(void* out, const void** inputs) {
   }
   for (int i = 0; i < 4; ++i)
     if (!inputs[i]) return oc::api_fail(OC_ERR_INVALID_ARGUMENT, "inputs[%d] is NULL", i);
+  if (reinterpret_cast<uintptr_t>(inputs[3]) % 4 != 0)
+    return oc::api_fail(OC_ERR_INVALID_ARGUMENT, "block_mask (inputs[3]) must be 4-byte aligned");
 
   // Workspace: [flags | active list | count | attention partials].
   const size_t off_idx = round256((size_t)nb);

@@ -753,12 +753,17 @@ static hipError_t launch_score_t(const ScoreParams& p, hipStream_t s) {
 // head_dim 256 does: C3's scoring pass with logits 208 -> 190 us, without 176 ->
 // 165 us at the same bytes (the per-tile merge, reductions and bound are
 // shared by twice the keys).
+// The second head's lane offset (its head stride plus the lane's column, in
+// bytes) must fit the 32-bit lane offset next to 64 token rows (< 2^31, checked
+// by the API), so pairs are formed only for head strides under 2^30 bytes.
 template <int DT>
 static hipError_t launch_score_dt(const ScoreParams& p, hipStream_t s) {
   const int lpr = p.head_dim / Elt<DT>::VEC;
+  const bool pairs = p.num_kv_heads % 2 == 0 && p.k_head_stride >= 0 &&
+                     p.k_head_stride * (int64_t)(16 / Elt<DT>::VEC) < ((int64_t)1 << 30);
   switch (lpr) {
-    case 8: return p.num_kv_heads % 2 == 0 ? launch_score_t<DT, 16, 2>(p, s) : launch_score_t<DT, 8>(p, s);
-    case 16: return p.num_kv_heads % 2 == 0 ? launch_score_t<DT, 32, 2>(p, s) : launch_score_t<DT, 16>(p, s);
+    case 8: return pairs ? launch_score_t<DT, 16, 2>(p, s) : launch_score_t<DT, 8>(p, s);
+    case 16: return pairs ? launch_score_t<DT, 32, 2>(p, s) : launch_score_t<DT, 16>(p, s);
     case 32: return launch_score_t<DT, 32>(p, s);
     case 64: return launch_score_t<DT, 64>(p, s);
     case 128: return launch_score_t<DT, 128>(p, s);

@@ -112,6 +112,23 @@ class TestBands:
         z = oc.compute_spectral_decay_ratio(kd)
         np.testing.assert_allclose(np32(z), O.spectral_decay_ratio(kref), rtol=1e-5)
 
+    @pytest.mark.parametrize("d,dtype", [(128, torch.bfloat16), (64, torch.float32)])
+    def test_head_major_storage(self, dev, d, dtype):
+        """Keys stored head-major ((H, S, D) memory, viewed as (S, H, D)): the
+        tile's second head is a head stride away rather than the next D
+        elements.  Scores and bounds equal the contiguous layout's bit for bit
+        (same values, same summation order)."""
+        from orthocache_amd import _ops
+
+        rng = np.random.default_rng(d)
+        keys = to_dev(rng.standard_normal((2048, 4, d)) + 0.3, dev, dtype)
+        q = to_dev(rng.standard_normal((1, 8, d)), dev, dtype)
+        hm = keys.permute(1, 0, 2).contiguous().permute(1, 0, 2)
+        assert hm.stride(1) == 2048 * d
+        a, b = _ops.score(keys, q, want_bands=True), _ops.score(hm, q, want_bands=True)
+        for name in ("tau_max", "zeta", "dc", "e_low", "e_mid", "e_high", "e_ac"):
+            assert torch.equal(getattr(a, name), getattr(b, name)), name
+
     def test_gate6_golden(self, dev):
         import orthocache_amd as oc
         from tests.test_oracle import GATE6_AC_A, GATE6_AC_B, GATE6_ZETA_B_MEAN, gate6_blocks
