@@ -1065,8 +1065,11 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
 // exp2(m_j - M) staged in LDS (and l = sum w_j l_j), and each thread
 // accumulates its output elements over the batch in partial order, so the
 // result is deterministic.  An empty list (or only empty pieces, m = -inf)
-// gives zeros.
+// gives zeros.  Lists of at most kListFast pieces (C3: all of them) skip the
+// staging: each thread requests every piece's (m, l) and its own elements'
+// partials together and merges in registers (C3 combine 10.45 -> 9.40 us).
 constexpr int kListBatch = 256;  // partials whose weights are staged per round
+constexpr int kListFast = 8;     // lists of at most this many pieces merge in registers
 
 __global__ __launch_bounds__(256) void combine_lists_kernel(AttendParams p) {
   constexpr int NWS = 1;                        // partials per piece (one per workgroup)
@@ -1091,6 +1094,78 @@ __global__ __launch_bounds__(256) void combine_lists_kernel(AttendParams p) {
   auto ml_at = [&](int j, int g) {
     return *reinterpret_cast<const float2*>(p.part_ml + ((i0 + j) * kQG + g) * 2);
   };
+  auto store_out = [&](int e, float v) {
+    const int g = e / D, d = e - g * D;
+    const int st = g / p.group, gg = g - st * p.group;
+    const int64_t orow = (int64_t)seg * p.out_seg_stride + (int64_t)st * p.out_tok_stride +
+                         (int64_t)(h * p.group + gg) * p.out_head_stride;
+    store_elt(p.out_dtype, p.out, orow + d, v);
+  };
+
+  // Few pieces (the common case): every thread requests all the pieces'
+  // (m, l) and its own output elements' partials at once and merges them in
+  // registers, with no barrier after the list offsets.
+  if (n <= kListFast) {
+    float mv[kListFast][MQ], lv[kListFast][MQ], ov[kListFast][EPT];
+#pragma unroll
+    for (int j = 0; j < kListFast; ++j) {
+      const int jc = min(j, max(n - 1, 0));
+#pragma unroll
+      for (int g = 0; g < MQ; ++g) {
+        const float2 ml = ml_at(jc, min(g, nq - 1));
+        mv[j][g] = ml.x;
+        lv[j][g] = ml.y;
+      }
+#pragma unroll
+      for (int k = 0; k < EPT; ++k) {
+        const int e = min(t + 256 * k, nq * D - 1);
+        const int g = e / D, d = e - g * D;
+        ov[j][k] = p.part_o[((i0 + jc) * kQG + g) * D + d];
+      }
+    }
+    float M[MQ], lsum[MQ];
+#pragma unroll
+    for (int g = 0; g < MQ; ++g) {
+      M[g] = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < kListFast; ++j) M[g] = fmaxf(M[g], j < n ? mv[j][g] : -INFINITY);
+      lsum[g] = 0.f;
+    }
+    float acc[EPT];
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) acc[k] = 0.f;
+#pragma unroll
+    for (int j = 0; j < kListFast; ++j) {
+      if (j < n) {
+        float w[MQ];
+#pragma unroll
+        for (int g = 0; g < MQ; ++g) {
+          w[g] = (mv[j][g] == -INFINITY) ? 0.f : exp2f(mv[j][g] - M[g]);
+          lsum[g] = fmaf(w[g], lv[j][g], lsum[g]);
+        }
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) {
+          const int g = min(t + 256 * k, nq * D - 1) / D;
+          float wg = w[0];
+#pragma unroll
+          for (int gg = 1; gg < MQ; ++gg) wg = g == gg ? w[gg] : wg;
+          acc[k] = fmaf(wg, ov[j][k], acc[k]);
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const int e = t + 256 * k;
+      if (e < nq * D) {
+        const int g = e / D;
+        float lg = lsum[0];
+#pragma unroll
+        for (int gg = 1; gg < MQ; ++gg) lg = g == gg ? lsum[gg] : lg;
+        store_out(e, lg == 0.f ? 0.f : acc[k] / lg);
+      }
+    }
+    return;
+  }
 
   float mx[MQ];
 #pragma unroll
@@ -1148,11 +1223,8 @@ __global__ __launch_bounds__(256) void combine_lists_kernel(AttendParams p) {
   for (int k = 0; k < EPT; ++k) {
     const int e = t + 256 * k;
     if (e < nq * D) {
-      const int g = e / D, d = e - g * D;
-      const int st = g / p.group, gg = g - st * p.group;
-      const int64_t orow = (int64_t)seg * p.out_seg_stride + (int64_t)st * p.out_tok_stride +
-                           (int64_t)(h * p.group + gg) * p.out_head_stride;
-      store_elt(p.out_dtype, p.out, orow + d, lsum[g] == 0.f ? 0.f : acc[k] / lsum[g]);
+      const int g = e / D;
+      store_out(e, lsum[g] == 0.f ? 0.f : acc[k] / lsum[g]);
     }
   }
 }
