@@ -9,11 +9,12 @@
 // are dense contractions (chunked prefill).
 //
 // Work decomposition: a workgroup (8 waves for head_dim 128, 4 for 64; 32
-// query rows per wave, so each staged K / V^T tile serves 256 or 128 rows)
+// query rows per wave, so each staged K / V tile serves 256 or 128 rows)
 // takes one query tile of a (segment, kv head) and a contiguous range of the
-// list's 64-key tiles (the
-// tile range is split `nsplit` ways so the grid fills the chip); it writes a
-// partial (m, l, O) per row and prefill_combine_kernel merges the splits.
+// list's 64-key tiles (the tile range is split `nsplit` ways so the grid
+// fills the chip); it writes a partial (m, l, O) per row, and
+// prefill_combine_half_kernel (16-bit outputs, fp16 partials) or
+// prefill_combine_kernel (fp32 outputs, fp32 partials) merges the splits.
 //
 // Per wave: 32 query rows, one per lane pair (lane l and l^32 hold row l%32).
 // With v_mfma_f32_32x32x16 (A 32x16, B 16x32, fp32 C 32x32):
