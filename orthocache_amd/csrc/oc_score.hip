@@ -21,10 +21,11 @@
 // of squares (shifted sums per thread, Chan merge across threads), so a large
 // block mean does not cancel it away.
 //
-// One workgroup (256 threads) scores one (block, kv head) tile of 512 x D.
-// Lanes are laid out LPR per token row (16-byte loads along D, coalesced);
-// NSLOT = 256/LPR row slots each walk 64/NSLOT values of l, loading the eight
-// rows 64k + l together.
+// One workgroup (256 threads) scores one tile: 512 token rows of one kv head,
+// or of two adjacent kv heads side by side when a head's row is 128 or 256
+// bytes (HPT = 2; per-head sums are kept apart).  Lanes are laid out LPR per
+// tile row (16-byte loads along D, coalesced); NSLOT = 256/LPR row slots each
+// walk 64/NSLOT values of l, loading the eight rows 64k + l together.
 //
 // Optionally (NQL > 0, decode with at most 4 query rows per kv head) the same
 // pass also forms the attention logits q.k of every key row it streams: the
