@@ -73,6 +73,25 @@ def event_time_us(fn, reps, torch):
     return start.elapsed_time(stop) * 1000.0 / reps
 
 
+def copy_bandwidth(torch, dev, mib=1024, reps=20):
+    """The box's achievable copy bandwidth, reported beside the published
+    peak: a device-to-device copy of `mib` MiB (torch's copy kernel), read +
+    write bytes over the HIP-event time of `reps` copies, after two untimed
+    ones.  A copy mixes reads and writes and runs below what the read-dominated
+    scoring pass reaches, so the published peak stays the roofline's."""
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    us = event_time_us(lambda: dst.copy_(src), reps, torch)
+    del src, dst
+    moved = 2 * mib * (1 << 20)
+    return {"gbps": round(moved / (us * 1e-6) / 1e9, 1), "bytes_per_copy": moved, "us_per_copy": round(us, 2),
+            "method": f"torch copy_ of {mib} MiB fp32 on the device (read + write bytes), HIP events, "
+                      f"mean over {reps} copies"}
+
+
 def _score_kernel_name(d: int, hkv: int, nq_pad: int) -> str:
     """The scoring kernel instantiation the library launches for bf16 keys and
     queries (oc_score.hip launch_score_dt): heads with 128- or 256-byte rows go
@@ -243,6 +262,7 @@ def main():
     compact_us = event_time_us(compact_fn, args.kernel_reps, torch) if compact_fn else 0.0
     attend_us = event_time_us(attend_fn, args.kernel_reps, torch)
     print(f"bench: timed {args.steps} steps", file=sys.stderr, flush=True)
+    copy = copy_bandwidth(torch, dev)
 
     s, hkv, d = wl.k.shape
     nb = s // 512
@@ -317,6 +337,7 @@ def main():
                      "traffic": traffic, "traffic_source": traffic_src,
                      "algorithmic_bytes": score_model_bytes, "logits_store_bytes": logit_bytes,
                      "kernel_us": round(score_us, 2)},
+        "hbm_copy": copy,
     }
     if not args.no_cpu:
         try:
@@ -512,6 +533,7 @@ def run_c3(args, torch, dev):
                           "achieved": round(score_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": round(score_gbs / PEAK_HBM_GBS, 4), "traffic": None,
                           "algorithmic_bytes": score_bytes, "kernel_us": round(kus["score"], 2)}}
+    extra["hbm_copy"] = copy_bandwidth(torch, dev)
     if not args.no_cpu:
         try:
             extra["cpu_baseline"] = cpu_baseline_segments(wl, tau_t.cpu().numpy(), zmax_t.cpu().numpy(),
@@ -592,6 +614,7 @@ def run_c5(args, torch, dev):
                           "achieved": round(score_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": round(score_gbs / PEAK_HBM_GBS, 4), "traffic": None,
                           "algorithmic_bytes": score_bytes, "kernel_us": round(score_us, 2)}}
+    extra["hbm_copy"] = copy_bandwidth(torch, dev)
     if not args.no_cpu:
         try:
             extra["cpu_baseline"] = cpu_baseline_segments(wl, tau_t.cpu().numpy(), zmax_t.cpu().numpy(),
