@@ -1,0 +1,101 @@
+"""GPU parity by property-based fuzzing: the two-gate mask and compaction.
+
+Hypothesis draws score arrays and thresholds whose values come partly from a
+pool of edge cases (NaN, +-inf, +-0, subnormals, values one ulp either side of
+1, the largest finite floats) and partly from all fp32 values, so ties at a
+threshold, NaN scores, NaN thresholds and empty or full masks all occur.  The
+GPU's mask, active-first permutation and count (oc_mask_compact) must equal
+the oracle's bit for bit: mask_from_scores over the NaN-propagating maximum of
+the partial maxima (spectral_energy.py:180-234: jnp.max, then fp32 compares),
+then stream_compact_indices (compaction.py:65-82).  One segment with 1-3
+partial maxima per score, and ragged segments with per-segment thresholds.
+Deterministic (derandomize), no example database.
+"""
+
+import numpy as np
+import pytest
+import torch
+from hypothesis import HealthCheck, given, settings
+from hypothesis import strategies as st
+from hypothesis.extra import numpy as hnp
+
+from oracle import oc_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+F32 = np.float32
+POOL = [float(x) for x in (-np.inf, np.inf, np.nan, -0.0, 0.0, 1e-45, -1e-45, 1e-39, -1.5, 1.0,
+                           np.nextafter(F32(1), F32(2)), np.nextafter(F32(1), F32(0)), 2.5, 7.0,
+                           np.finfo(F32).max, -np.finfo(F32).max)]
+ELEMS = st.one_of(st.sampled_from(POOL), st.floats(width=32, allow_nan=True, allow_infinity=True))
+THRESH = st.one_of(st.sampled_from(POOL), st.floats(width=32, allow_nan=True, allow_infinity=True))
+FUZZ = settings(derandomize=True, database=None, max_examples=60, deadline=None,
+                suppress_health_check=[HealthCheck.too_slow, HealthCheck.data_too_large])
+
+
+def _dev():
+    return torch.device("cuda:0")
+
+
+@st.composite
+def one_segment(draw):
+    nb = draw(st.integers(1, 160))
+    h = draw(st.integers(1, 8))
+    parts = draw(st.integers(1, 3))
+    tm = draw(hnp.arrays(F32, (parts, nb, h), elements=ELEMS))
+    z = draw(hnp.arrays(F32, (nb, h), elements=ELEMS))
+    return tm, z, draw(THRESH), draw(THRESH)
+
+
+@given(one_segment())
+@FUZZ
+def test_fuzz_mask_compact(case):
+    from orthocache_amd import _ops
+
+    tm, z, tau, zmax = case
+    parts, nb, h = tm.shape
+    dev = _dev()
+    c = _ops.mask_compact(num_blocks=nb, num_kv_heads=h, device=dev, tau_max=torch.from_numpy(tm).to(dev),
+                          zeta=torch.from_numpy(z).to(dev), tau=tau, zeta_max=zmax, want_mask=True)
+    torch.cuda.synchronize()
+    exp = O.mask_from_scores(O.nanmax_axis0(tm), z, tau, zmax)
+    order, n = O.stream_compact_indices(exp)
+    np.testing.assert_array_equal(c.mask.cpu().numpy(), exp)
+    np.testing.assert_array_equal(c.indices.cpu().numpy(), order)
+    assert int(c.num_active[0]) == n
+
+
+@st.composite
+def segments(draw):
+    lens = draw(st.lists(st.integers(1, 40), min_size=2, max_size=6))
+    h = draw(st.integers(1, 4))
+    nb = sum(lens)
+    tm = draw(hnp.arrays(F32, (nb, h), elements=ELEMS))
+    z = draw(hnp.arrays(F32, (nb, h), elements=ELEMS))
+    taus = draw(hnp.arrays(F32, (len(lens),), elements=THRESH))
+    zmaxs = draw(hnp.arrays(F32, (len(lens),), elements=THRESH))
+    return lens, tm, z, taus, zmaxs
+
+
+@given(segments())
+@FUZZ
+def test_fuzz_mask_compact_segments(case):
+    from orthocache_amd import _ops
+
+    lens, tm, z, taus, zmaxs = case
+    nb, h = tm.shape
+    dev = _dev()
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    c = _ops.mask_compact(num_blocks=nb, num_kv_heads=h, device=dev, tau_max=torch.from_numpy(tm).to(dev),
+                          zeta=torch.from_numpy(z).to(dev), tau=torch.from_numpy(taus).to(dev),
+                          zeta_max=torch.from_numpy(zmaxs).to(dev), want_mask=True,
+                          cu_blocks=torch.from_numpy(cu).to(dev), num_segments=len(lens))
+    torch.cuda.synchronize()
+    mask, idx, cnt = c.mask.cpu().numpy(), c.indices.cpu().numpy(), c.num_active.cpu().numpy()
+    for s in range(len(lens)):
+        lo, hi = cu[s], cu[s + 1]
+        exp = O.mask_from_scores(tm[lo:hi], z[lo:hi], float(taus[s]), float(zmaxs[s]))
+        order, n = O.stream_compact_indices(exp)
+        np.testing.assert_array_equal(mask[lo:hi], exp)
+        np.testing.assert_array_equal(idx[lo:hi], order)
+        assert int(cnt[s]) == n

@@ -63,6 +63,38 @@ class TestPort:
         np.testing.assert_array_equal(idx, order)
         assert n == n_ref
 
+    def test_compact_fuzz_matches_oracle(self, port):
+        """Property-based: NaN, +-inf, +-0, subnormal and tied scores and
+        thresholds; the port's mask, permutation and count equal the NumPy
+        oracle's bit for bit."""
+        from hypothesis import HealthCheck, given, settings
+        from hypothesis import strategies as st
+        from hypothesis.extra import numpy as hnp
+
+        pool = [float(x) for x in (-np.inf, np.inf, np.nan, -0.0, 0.0, 1e-45, -1e-45, 1.0,
+                                   np.nextafter(np.float32(1), np.float32(2)), 2.5)]
+        elems = st.one_of(st.sampled_from(pool), st.floats(width=32, allow_nan=True, allow_infinity=True))
+
+        @st.composite
+        def case(draw):
+            nb, h = draw(st.integers(1, 120)), draw(st.integers(1, 6))
+            return (draw(hnp.arrays(np.float32, (nb, h), elements=elems)),
+                    draw(hnp.arrays(np.float32, (nb, h), elements=elems)), draw(elems), draw(elems))
+
+        @given(case())
+        @settings(derandomize=True, database=None, max_examples=80, deadline=None,
+                  suppress_health_check=[HealthCheck.too_slow, HealthCheck.data_too_large])
+        def check(c):
+            tm, z, tau, zmax = c
+            mask, idx, n = ON.port_compact(tm, z, tau, zmax)
+            exp = O.mask_from_scores(tm, z, tau, zmax)
+            np.testing.assert_array_equal(mask, exp)
+            order, n_ref = O.stream_compact_indices(exp)
+            np.testing.assert_array_equal(idx, order)
+            assert n == n_ref
+
+        check()
+
     def test_attend_matches_oracle(self, port):
         rng = np.random.default_rng(7)
         q = rng.standard_normal((2, 4, 64)).astype(np.float32)
