@@ -8,8 +8,9 @@ GPU's mask, active-first permutation and count (oc_mask_compact) must equal
 the oracle's bit for bit: mask_from_scores over the NaN-propagating maximum of
 the partial maxima (spectral_energy.py:180-234: jnp.max, then fp32 compares),
 then stream_compact_indices (compaction.py:65-82).  One segment with 1-3
-partial maxima per score, and ragged segments with per-segment thresholds.
-Deterministic (derandomize), no example database.
+partial maxima per score, and ragged segments with per-segment thresholds;
+and given masks with the per-head lists.  Deterministic (derandomize), no
+example database.
 """
 
 import numpy as np
@@ -99,3 +100,36 @@ def test_fuzz_mask_compact_segments(case):
         np.testing.assert_array_equal(mask[lo:hi], exp)
         np.testing.assert_array_equal(idx[lo:hi], order)
         assert int(cnt[s]) == n
+
+
+@st.composite
+def given_masks(draw):
+    nb = draw(st.integers(1, 600))
+    h = draw(st.integers(1, 8))
+    density = draw(st.sampled_from([0.0, 0.01, 0.1, 0.5, 1.0]))
+    seed = draw(st.integers(0, 2**31 - 1))
+    m = np.random.default_rng(seed).random((nb, h)) < density
+    return m
+
+
+@given(given_masks())
+@FUZZ
+def test_fuzz_given_mask_head_lists(m):
+    """A given (block, head) mask: the unified active-first permutation and
+    count (compaction.py:65-82) and every head's own list (the per-head
+    compaction behind the predicated per-head attention, sparse_attention.py:5-64)."""
+    from orthocache_amd import _ops
+
+    nb, h = m.shape
+    dev = _dev()
+    c = _ops.mask_compact(num_blocks=nb, num_kv_heads=h, device=dev, mask_in=torch.from_numpy(m).to(dev),
+                          want_head_lists=True)
+    torch.cuda.synchronize()
+    order, n = O.stream_compact_indices(m)
+    np.testing.assert_array_equal(c.indices.cpu().numpy(), order)
+    assert int(c.num_active[0]) == n
+    hi, hn = c.head_indices.cpu().numpy(), c.head_num_active.cpu().numpy()
+    for k in range(h):
+        oh, nh = O.stream_compact_indices(m[:, k])
+        np.testing.assert_array_equal(hi[k], oh)
+        assert int(hn[0, k]) == nh
