@@ -1357,10 +1357,14 @@ static hipError_t launch_stream(const AttendParams& p, hipStream_t s) {
   }
 }
 
-// Which streaming form applies and its `splits`: about one workgroup per CU.
-// C2 at 90%, split form with logits, attention + combine: 128, 256, 512, 1024
-// and 2048 workgroups gave 26.1, 19.1, 19.7, 21.4 and 23.2 us (a two-chunk
-// ring).  At most 4 query rows per kv head and whole 512-token blocks; keys
+// Which streaming form applies and its `splits`: about one workgroup per CU,
+// two where the kernel fits two.  C2 at 90%, split form with logits,
+// attention + combine: 128, 256, 512, 1024 and 2048 workgroups gave 26.1,
+// 19.1, 19.7, 21.4 and 23.2 us (a two-chunk ring).  Four query rows with
+// logits fit two workgroups per CU, and both forms then take 512: one segment
+// of 425 blocks, 8 kv heads, head_dim 128, split form with 256 workgroups
+// 100.1 + 5.0 us (attention + combine), with 512 85.9 + 5.0 us.  At most 4
+// query rows per kv head and whole 512-token blocks; keys
 // and values (no logits) also need a block of whole chunks.  The split form
 // needs one segment and a unified list (its list fits LDS); the ranges form
 // takes any lists, with few enough workgroups that its w + L partial slots
@@ -1373,16 +1377,18 @@ void attend_stream_plan(AttendParams& p) {
       p.sq * p.group > kLogitsMaxQ || (p.keep && p.total_blocks > kMaxLists) || kBlock % p.chunk != 0)
     return;
   const int64_t chunks = (int64_t)p.total_blocks * p.nchunk;
+  // Workgroups: one per CU, two where the kernel fits two (four query rows
+  // with logits).
+  const int64_t cap = (p.logits && attend_nq_bucket(p.sq * p.group) == 4) ? 512 : 256;
   if (!p.cu_blocks && !p.per_head && !p.uniform && p.total_blocks <= kMaxLists) {
-    int64_t sp = 256 / p.num_kv_heads;
+    int64_t sp = cap / p.num_kv_heads;
     sp = sp < 1 ? 1 : (sp > 64 ? 64 : sp);
     p.stream = kStreamSplit;
     p.splits = (int)(sp < chunks ? sp : chunks);
     return;
   }
-  // Ranges-form workgroups: one per CU, two where the kernel fits two (four
-  // query rows with logits: C3 layer 350.5 -> 345.5 us).
-  const int64_t cap = (p.logits && attend_nq_bucket(p.sq * p.group) == 4) ? 512 : 256;
+  // Ranges form (two workgroups per CU for four query rows with logits: C3
+  // layer 350.5 -> 345.5 us).
   const int64_t room = attend_max_items(p) - nl;
   const int64_t g = room < cap ? room : cap;
   if (g >= 1 && !p.keep) {
