@@ -1060,16 +1060,22 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
 // columns: C3 has 8 times as many workgroups; C3 layer 346 -> 341 us).  The
 // split form keeps combine_kernel: with one list per kv head (C2: 16) this
 // kernel's few workgroups each walk a long chain of loads (C2 layer 108.0 ->
-// 111.3 us).  First the row maxima M of the
+// 111.3 us).  Lists of at most kListRegMax pieces merge in registers,
+// kListFast pieces per round: each thread requests the round's (m, l) and its
+// own elements' partials together, then folds them in with a running maximum
+// (C3, one round: combine 10.45 -> 9.40 -> 8.8 us; eight segments of 32
+// retained blocks, 8 kv heads, 8-9 pieces per list: 9.3 -> 8.3 us).  Each
+// further round waits for its own loads, which the staged form below
+// overlaps (16-17 and 33 pieces per list: 11.4 -> 12.6 and 12.8 -> 18.0 us
+// in rounds), so longer lists are staged: first the row maxima M of the
 // pieces' references m, then, a batch of partials at a time, the weights
 // exp2(m_j - M) staged in LDS (and l = sum w_j l_j), and each thread
-// accumulates its output elements over the batch in partial order, so the
-// result is deterministic.  An empty list (or only empty pieces, m = -inf)
-// gives zeros.  Lists of at most kListFast pieces (C3: all of them) skip the
-// staging: each thread requests every piece's (m, l) and its own elements'
-// partials together and merges in registers (C3 combine 10.45 -> 9.40 us).
+// accumulates its output elements over the batch.  Either way the pieces are
+// taken in partial order, so the result is deterministic.  An empty list (or
+// only empty pieces, m = -inf) gives zeros.
 constexpr int kListBatch = 256;  // partials whose weights are staged per round
-constexpr int kListFast = 8;     // lists of at most this many pieces merge in registers
+constexpr int kListFast = 8;     // pieces per register round
+constexpr int kListRegMax = 12;  // lists of at most this many pieces merge in registers
 
 __global__ __launch_bounds__(256) void combine_lists_kernel(AttendParams p) {
   constexpr int NWS = 1;                        // partials per piece (one per workgroup)
@@ -1102,54 +1108,71 @@ __global__ __launch_bounds__(256) void combine_lists_kernel(AttendParams p) {
     store_elt(p.out_dtype, p.out, orow + d, v);
   };
 
-  // Few pieces (the common case): every thread requests all the pieces'
-  // (m, l) and its own output elements' partials at once and merges them in
-  // registers, with no barrier after the list offsets.
-  if (n <= kListFast) {
-    float mv[kListFast][MQ], lv[kListFast][MQ], ov[kListFast][EPT];
+  // Few pieces (the common case; C3 takes one round of kListFast): per round
+  // every thread requests the pieces' (m, l) and its own output elements'
+  // partials at once and merges them in registers (running maximum, sums
+  // rescaled when it moves), with no barrier after the list offsets.
+  if (n <= kListRegMax) {
+    float M[MQ], lsum[MQ], acc[EPT];
 #pragma unroll
-    for (int j = 0; j < kListFast; ++j) {
-      const int jc = min(j, max(n - 1, 0));
-#pragma unroll
-      for (int g = 0; g < MQ; ++g) {
-        const float2 ml = ml_at(jc, min(g, nq - 1));
-        mv[j][g] = ml.x;
-        lv[j][g] = ml.y;
-      }
-#pragma unroll
-      for (int k = 0; k < EPT; ++k) {
-        const int e = min(t + 256 * k, nq * D - 1);
-        const int g = e / D, d = e - g * D;
-        ov[j][k] = p.part_o[((i0 + jc) * kQG + g) * D + d];
-      }
-    }
-    float M[MQ], lsum[MQ];
-#pragma unroll
-    for (int g = 0; g < MQ; ++g) {
-      M[g] = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < kListFast; ++j) M[g] = fmaxf(M[g], j < n ? mv[j][g] : -INFINITY);
-      lsum[g] = 0.f;
-    }
-    float acc[EPT];
+    for (int g = 0; g < MQ; ++g) { M[g] = -INFINITY; lsum[g] = 0.f; }
 #pragma unroll
     for (int k = 0; k < EPT; ++k) acc[k] = 0.f;
+    // Query row of each of the thread's output elements.
+    int gk[EPT];
 #pragma unroll
-    for (int j = 0; j < kListFast; ++j) {
-      if (j < n) {
-        float w[MQ];
+    for (int k = 0; k < EPT; ++k) gk[k] = min(t + 256 * k, nq * D - 1) / D;
+    for (int r0 = 0; r0 < n; r0 += kListFast) {
+      float mv[kListFast][MQ], lv[kListFast][MQ], ov[kListFast][EPT];
+#pragma unroll
+      for (int j = 0; j < kListFast; ++j) {
+        const int jc = min(r0 + j, n - 1);
 #pragma unroll
         for (int g = 0; g < MQ; ++g) {
-          w[g] = (mv[j][g] == -INFINITY) ? 0.f : exp2f(mv[j][g] - M[g]);
-          lsum[g] = fmaf(w[g], lv[j][g], lsum[g]);
+          const float2 ml = ml_at(jc, min(g, nq - 1));
+          mv[j][g] = ml.x;
+          lv[j][g] = ml.y;
         }
 #pragma unroll
         for (int k = 0; k < EPT; ++k) {
-          const int g = min(t + 256 * k, nq * D - 1) / D;
-          float wg = w[0];
+          const int e = min(t + 256 * k, nq * D - 1);
+          const int g = e / D, d = e - g * D;
+          ov[j][k] = p.part_o[((i0 + jc) * kQG + g) * D + d];
+        }
+      }
+      float bm[MQ], sc[MQ];
 #pragma unroll
-          for (int gg = 1; gg < MQ; ++gg) wg = g == gg ? w[gg] : wg;
-          acc[k] = fmaf(wg, ov[j][k], acc[k]);
+      for (int g = 0; g < MQ; ++g) {
+        bm[g] = M[g];
+#pragma unroll
+        for (int j = 0; j < kListFast; ++j) bm[g] = fmaxf(bm[g], r0 + j < n ? mv[j][g] : -INFINITY);
+        sc[g] = (M[g] == -INFINITY) ? 0.f : exp2f(M[g] - bm[g]);
+        lsum[g] *= sc[g];
+        M[g] = bm[g];
+      }
+#pragma unroll
+      for (int k = 0; k < EPT; ++k) {
+        float s = sc[0];
+#pragma unroll
+        for (int gg = 1; gg < MQ; ++gg) s = gk[k] == gg ? sc[gg] : s;
+        acc[k] *= s;
+      }
+#pragma unroll
+      for (int j = 0; j < kListFast; ++j) {
+        if (r0 + j < n) {
+          float w[MQ];
+#pragma unroll
+          for (int g = 0; g < MQ; ++g) {
+            w[g] = (mv[j][g] == -INFINITY) ? 0.f : exp2f(mv[j][g] - M[g]);
+            lsum[g] = fmaf(w[g], lv[j][g], lsum[g]);
+          }
+#pragma unroll
+          for (int k = 0; k < EPT; ++k) {
+            float wg = w[0];
+#pragma unroll
+            for (int gg = 1; gg < MQ; ++gg) wg = gk[k] == gg ? w[gg] : wg;
+            acc[k] = fmaf(wg, ov[j][k], acc[k]);
+          }
         }
       }
     }
@@ -1157,10 +1180,9 @@ __global__ __launch_bounds__(256) void combine_lists_kernel(AttendParams p) {
     for (int k = 0; k < EPT; ++k) {
       const int e = t + 256 * k;
       if (e < nq * D) {
-        const int g = e / D;
         float lg = lsum[0];
 #pragma unroll
-        for (int gg = 1; gg < MQ; ++gg) lg = g == gg ? lsum[gg] : lg;
+        for (int gg = 1; gg < MQ; ++gg) lg = gk[k] == gg ? lsum[gg] : lg;
         store_out(e, lg == 0.f ? 0.f : acc[k] / lg);
       }
     }
