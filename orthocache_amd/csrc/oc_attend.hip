@@ -508,7 +508,8 @@ struct Stream {
   // 242 VGPRs, two workgroups per CU, where three buffers
   // needed AGPR spill space and ran one.
   static constexpr int NB = (KV || NQ == 4) ? 2 : 3;
-  static_assert(NQ <= kLogitsMaxQ, "the streaming forms carry at most kLogitsMaxQ queries");
+  static_assert(KV ? NQ <= 2 * kLogitsMaxQ : NQ <= kLogitsMaxQ,
+                "the streaming forms carry at most kLogitsMaxQ queries with logits, twice that reading keys");
 
   struct State {
     float m[NQ], l[NQ], o[NQ][VEC];
@@ -1337,7 +1338,7 @@ static void launch_stream_k(const AttendParams& p, hipStream_t s) {
   if (p.stream == kStreamSplit) {
     hipLaunchKernelGGL((attend_split_kernel<DT, LPR, NQ, KV, QDT>), dim3(p.num_kv_heads * p.splits),
                        dim3(kAttendThreads), 0, s, p);
-  } else {
+  } else if constexpr (NQ <= kLogitsMaxQ) {  // the ranges form carries at most kLogitsMaxQ rows
     hipLaunchKernelGGL((attend_stream_kernel<DT, LPR, NQ, KV, QDT>), dim3(p.splits), dim3(kAttendThreads), 0, s, p);
   }
 }
@@ -1345,7 +1346,8 @@ static void launch_stream_k(const AttendParams& p, hipStream_t s) {
 template <int DT, int LPR, int NQ>
 static hipError_t launch_stream_nq(const AttendParams& p, hipStream_t s) {
   if (p.logits) {
-    launch_stream_k<DT, LPR, NQ, false, DT>(p, s);
+    if constexpr (NQ <= kLogitsMaxQ) launch_stream_k<DT, LPR, NQ, false, DT>(p, s);
+    else return hipErrorInvalidValue;
   } else if (p.q_dtype == DT) {
     launch_stream_k<DT, LPR, NQ, true, DT>(p, s);
   } else if (p.q_dtype == kF32) {
@@ -1363,6 +1365,7 @@ static hipError_t launch_stream_dt(const AttendParams& p, hipStream_t s) {
     case 1: e = launch_stream_nq<DT, LPR, 1>(p, s); break;
     case 2: e = launch_stream_nq<DT, LPR, 2>(p, s); break;
     case 4: e = launch_stream_nq<DT, LPR, 4>(p, s); break;
+    case 8: e = launch_stream_nq<DT, LPR, 8>(p, s); break;
     default: return hipErrorInvalidValue;
   }
   return e != hipSuccess ? e : hipGetLastError();
@@ -1385,18 +1388,23 @@ static hipError_t launch_stream(const AttendParams& p, hipStream_t s) {
 // 19.1, 19.7, 21.4 and 23.2 us (a two-chunk ring).  Four query rows with
 // logits fit two workgroups per CU, and both forms then take 512: one segment
 // of 425 blocks, 8 kv heads, head_dim 128, split form with 256 workgroups
-// 100.1 + 5.0 us (attention + combine), with 512 85.9 + 5.0 us.  At most 4
-// query rows per kv head and whole 512-token blocks; keys
-// and values (no logits) also need a block of whole chunks.  The split form
-// needs one segment and a unified list (its list fits LDS); the ranges form
-// takes any lists, with few enough workgroups that its w + L partial slots
-// fit the per-item workspace.
+// 100.1 + 5.0 us (attention + combine), with 512 85.9 + 5.0 us.  Whole
+// 512-token blocks and at most 4 query rows per kv head, or 5-8 in the split
+// form reading keys and values (8 rows, one segment of 256 blocks, 8 kv
+// heads, head_dim 128, as per-item work: 52.2 us at 26 retained blocks and
+// 200.8 us at 128; split form 29.8 and 92.3 us); keys and values (no logits)
+// also need a block of whole chunks.  The split form needs one segment and a
+// unified list (its list fits LDS); the ranges form takes any lists, with few
+// enough workgroups that its w + L partial slots fit the per-item workspace.
 void attend_stream_plan(AttendParams& p) {
   p.stream = kStreamNone;
   p.splits = 0;
   const int64_t nl = (int64_t)p.num_segments * p.num_kv_heads;
+  // 5-8 query rows per kv head: the split form reading keys and values only.
+  const bool wide = p.sq * p.group > kLogitsMaxQ;
   if (p.prefill || p.block_size != kBlock || p.total_blocks < 1 || nl > kMaxLists ||
-      p.sq * p.group > kLogitsMaxQ || (p.keep && p.total_blocks > kMaxLists) || kBlock % p.chunk != 0)
+      p.sq * p.group > 2 * kLogitsMaxQ || (wide && p.logits) || (p.keep && p.total_blocks > kMaxLists) ||
+      kBlock % p.chunk != 0)
     return;
   const int64_t chunks = (int64_t)p.total_blocks * p.nchunk;
   // Workgroups: one per CU, two where the kernel fits two (four query rows
@@ -1409,6 +1417,7 @@ void attend_stream_plan(AttendParams& p) {
     p.splits = (int)(sp < chunks ? sp : chunks);
     return;
   }
+  if (wide) return;
   // Ranges form (two workgroups per CU for four query rows with logits: C3
   // layer 350.5 -> 345.5 us).
   const int64_t room = attend_max_items(p) - nl;
