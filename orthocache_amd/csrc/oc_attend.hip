@@ -520,9 +520,15 @@ struct Stream {
     float sl[KV ? 1 : R][NQ];
     uint4 kw[KV ? R : 1];
   };
-  // The lane's query columns, pre-scaled by log2(e)/sqrt(d) (KV = true).
+  // The lane's query columns (KV = true).  With 16-bit keys and queries of
+  // the same type they stay packed (DOT2: packed dot products on the raw key
+  // words, the sums scaled by log2(e)/sqrt(d) after the lane reduction);
+  // otherwise they are widened and pre-scaled.
+  static constexpr bool DOT2 = KV && DT != kF32 && QDT == DT;
   struct Query {
-    float q[KV ? NQ : 1][VEC];
+    float q[KV && !DOT2 ? NQ : 1][VEC];
+    uint32_t qw[DOT2 ? NQ : 1][VEC / 2];
+    float scale;
   };
 
   __device__ __forceinline__ static void reset(State& st) {
@@ -581,15 +587,22 @@ struct Stream {
         const char* qp = reinterpret_cast<const char*>(p.q) +
                          ((int64_t)seg * p.q_seg_stride + (int64_t)st * p.q_tok_stride +
                           (int64_t)(h * p.group + gg) * p.q_head_stride + (int64_t)cc * VEC) * QSZ;
-        const float sc = g < nq ? p.logit_scale : 0.f;
+        if constexpr (DOT2) {
+          const uint4 w = ld16(qp);
 #pragma unroll
-        for (int e0 = 0; e0 < VEC; e0 += EQ::VEC) {
-          float tmp[EQ::VEC];
-          EQ::unpack(ld16(qp + e0 * QSZ), tmp);
+          for (int i = 0; i < VEC / 2; ++i) qr.qw[g][i] = g < nq ? word_of(w, i) : 0u;
+        } else {
+          const float sc = g < nq ? p.logit_scale : 0.f;
 #pragma unroll
-          for (int e = 0; e < EQ::VEC && e0 + e < VEC; ++e) qr.q[g][e0 + e] = tmp[e] * sc;
+          for (int e0 = 0; e0 < VEC; e0 += EQ::VEC) {
+            float tmp[EQ::VEC];
+            EQ::unpack(ld16(qp + e0 * QSZ), tmp);
+#pragma unroll
+            for (int e = 0; e < EQ::VEC && e0 + e < VEC; ++e) qr.q[g][e0 + e] = tmp[e] * sc;
+          }
         }
       }
+      qr.scale = p.logit_scale;
     }
   }
 
@@ -604,19 +617,35 @@ struct Stream {
     } else {
       constexpr int V = R * NQ;  // value index r * NQ + g
       float part[V];
+      if constexpr (DOT2) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        float kx[VEC];
-        E::unpack(b.kw[r], kx);
+        for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int g = 0; g < NQ; ++g) {
-          float d = 0.f;
+          for (int g = 0; g < NQ; ++g) {
+            float d = 0.f;
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) d = fmaf(qr.q[g][e], kx[e], d);
-          part[r * NQ + g] = d;
+            for (int w = 0; w < VEC / 2; ++w) d = dot2_acc<DT>(word_of(b.kw[r], w), qr.qw[g][w], d);
+            part[r * NQ + g] = d;
+          }
+      } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          float kx[VEC];
+          E::unpack(b.kw[r], kx);
+#pragma unroll
+          for (int g = 0; g < NQ; ++g) {
+            float d = 0.f;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) d = fmaf(qr.q[g][e], kx[e], d);
+            part[r * NQ + g] = d;
+          }
         }
       }
       Butterfly<V, V, LPR / 2, LPR>::run(part, cc);
+      if constexpr (DOT2) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) part[i] *= qr.scale;
+      }
       // Gather the V sums to every lane of the slot (width-LPR shuffles).
       if constexpr (V >= LPR) {
         constexpr int PL = V / LPR;  // lane s holds indices s * PL .. + PL
