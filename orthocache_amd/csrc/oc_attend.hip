@@ -576,13 +576,15 @@ struct Stream {
   }
 
   // The query rows of list (seg, h), this lane's VEC columns (KV = true).
-  __device__ __forceinline__ static void load_query(const AttendParams& p, int seg, int h, int cc, Query& qr) {
+  // q0: the first of the NQ query rows (the split form's query group).
+  __device__ __forceinline__ static void load_query(const AttendParams& p, int seg, int h, int cc, Query& qr,
+                                                    int q0 = 0) {
     if constexpr (KV) {
       constexpr int QSZ = (QDT == kF32) ? 4 : 2;
-      const int nq = p.sq * p.group;
+      const int nq = p.sq * p.group - q0;  // rows of this group and after it
 #pragma unroll
       for (int g = 0; g < NQ; ++g) {
-        const int qc = min(g, nq - 1);
+        const int qc = q0 + min(g, nq - 1);
         const int st = qc / p.group, gg = qc - st * p.group;
         const char* qp = reinterpret_cast<const char*>(p.q) +
                          ((int64_t)seg * p.q_seg_stride + (int64_t)st * p.q_tok_stride +
@@ -760,7 +762,10 @@ __global__ __launch_bounds__(kAttendThreads) void attend_split_kernel(AttendPara
 
   const int H = p.num_kv_heads;
   const int h = blockIdx.x % H;
-  const int split = blockIdx.x / H;
+  // Query group (more than kLogitsMaxQ rows per kv head): rows qg * NQ ...
+  constexpr bool kGroups = NQ > kLogitsMaxQ;
+  const int split = kGroups ? (blockIdx.x / H) % p.splits : blockIdx.x / H;
+  const int qg = kGroups ? blockIdx.x / (H * p.splits) : 0;
   const int t = threadIdx.x;
   const int cc = t % LPR;
   const int slot = t / LPR;
@@ -795,7 +800,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_split_kernel(AttendPara
   typename S::State st;
   S::reset(st);
   typename S::Query qr;
-  S::load_query(p, 0, h, cc, qr);
+  S::load_query(p, 0, h, cc, qr, qg * NQ);
   typename S::Buf buf[NB];
 #pragma unroll
   for (int j = 0; j < NB - 1; ++j)
@@ -820,7 +825,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_split_kernel(AttendPara
     }
   }
   __syncthreads();
-  const int64_t item = (int64_t)split * H + h;
+  const int64_t item = ((int64_t)qg * p.splits + split) * H + h;
   float* po = p.part_o + item * kQG * D;
   float* pml = p.part_ml + item * kQG * 2;
   for (int e = t; e < NQ * D; e += blockDim.x) {
@@ -1026,7 +1031,7 @@ __global__ __launch_bounds__(256) void combine_kernel(AttendParams p) {
   const bool one_unit = !p.per_head && p.num_segments == 1;
   const int base = (one_unit || p.stream != kStreamNone) ? 0 : s_off[p.per_head ? list : seg];
   int64_t i0, istr;
-  if (p.stream == kStreamSplit) { i0 = h; istr = H; }
+  if (p.stream == kStreamSplit) { i0 = (int64_t)qg * p.splits * H + h; istr = H; }
   else if (p.per_head) { i0 = base + qg; istr = nqg; }
   else { i0 = (int64_t)base + (int64_t)qg * H + h; istr = (int64_t)nqg * H; }
   auto item_of = [&](int j) -> int64_t { return i0 + (int64_t)j * istr; };
@@ -1362,10 +1367,19 @@ int64_t attend_max_items(const AttendParams& p) {
   return (int64_t)p.num_kv_heads * p.total_blocks * p.nchunk * nqg;
 }
 
+// Query groups of the split form: kQG rows each above kLogitsMaxQ rows per
+// kv head (every group's workgroups read the same keys and values, the second
+// time mostly from the infinity cache), one group otherwise.
+constexpr int kSplitMaxRows = 2 * kQG;
+static int split_qgroups(const AttendParams& p) {
+  const int nq = p.sq * p.group;
+  return nq > kLogitsMaxQ ? (nq + kQG - 1) / kQG : 1;
+}
+
 template <int DT, int LPR, int NQ, bool KV, int QDT>
 static void launch_stream_k(const AttendParams& p, hipStream_t s) {
   if (p.stream == kStreamSplit) {
-    hipLaunchKernelGGL((attend_split_kernel<DT, LPR, NQ, KV, QDT>), dim3(p.num_kv_heads * p.splits),
+    hipLaunchKernelGGL((attend_split_kernel<DT, LPR, NQ, KV, QDT>), dim3(p.num_kv_heads * p.splits * split_qgroups(p)),
                        dim3(kAttendThreads), 0, s, p);
   } else if constexpr (NQ <= kLogitsMaxQ) {  // the ranges form carries at most kLogitsMaxQ rows
     hipLaunchKernelGGL((attend_stream_kernel<DT, LPR, NQ, KV, QDT>), dim3(p.splits), dim3(kAttendThreads), 0, s, p);
@@ -1418,10 +1432,11 @@ static hipError_t launch_stream(const AttendParams& p, hipStream_t s) {
 // logits fit two workgroups per CU, and both forms then take 512: one segment
 // of 425 blocks, 8 kv heads, head_dim 128, split form with 256 workgroups
 // 100.1 + 5.0 us (attention + combine), with 512 85.9 + 5.0 us.  Whole
-// 512-token blocks and at most 4 query rows per kv head, or 5-8 in the split
-// form reading keys and values (8 rows, one segment of 256 blocks, 8 kv
-// heads, head_dim 128, as per-item work: 52.2 us at 26 retained blocks and
-// 200.8 us at 128; split form 29.8 and 92.3 us); keys and values (no logits)
+// 512-token blocks and at most 4 query rows per kv head, or 5-16 in the split
+// form reading keys and values, in groups of 8 rows (8 rows, one segment of
+// 256 blocks, 8 kv heads, head_dim 128, as per-item work: 52.2 us at 26
+// retained blocks and 200.8 us at 128; split form 29.8 and 92.3 us; 16 rows at
+// 26 blocks 84.4 -> 40.8 us); keys and values (no logits)
 // also need a block of whole chunks.  The split form needs one segment and a
 // unified list (its list fits LDS); the ranges form takes any lists, with few
 // enough workgroups that its w + L partial slots fit the per-item workspace.
@@ -1429,10 +1444,11 @@ void attend_stream_plan(AttendParams& p) {
   p.stream = kStreamNone;
   p.splits = 0;
   const int64_t nl = (int64_t)p.num_segments * p.num_kv_heads;
-  // 5-8 query rows per kv head: the split form reading keys and values only.
+  // 5-16 query rows per kv head: the split form reading keys and values
+  // only, in groups of kQG rows.
   const bool wide = p.sq * p.group > kLogitsMaxQ;
   if (p.prefill || p.block_size != kBlock || p.total_blocks < 1 || nl > kMaxLists ||
-      p.sq * p.group > 2 * kLogitsMaxQ || (wide && p.logits) || (p.keep && p.total_blocks > kMaxLists) ||
+      p.sq * p.group > kSplitMaxRows || (wide && p.logits) || (p.keep && p.total_blocks > kMaxLists) ||
       kBlock % p.chunk != 0)
     return;
   const int64_t chunks = (int64_t)p.total_blocks * p.nchunk;
@@ -1440,7 +1456,7 @@ void attend_stream_plan(AttendParams& p) {
   // with logits).
   const int64_t cap = (p.logits && attend_nq_bucket(p.sq * p.group) == 4) ? 512 : 256;
   if (!p.cu_blocks && !p.per_head && !p.uniform && p.total_blocks <= kMaxLists) {
-    int64_t sp = cap / p.num_kv_heads;
+    int64_t sp = cap / ((int64_t)p.num_kv_heads * split_qgroups(p));
     sp = sp < 1 ? 1 : (sp > 64 ? 64 : sp);
     p.stream = kStreamSplit;
     p.splits = (int)(sp < chunks ? sp : chunks);
@@ -1467,7 +1483,7 @@ void attend_stream_plan(AttendParams& p) {
 int64_t attend_partial_slots(const AttendParams& p_in) {
   AttendParams p = p_in;
   attend_stream_plan(p);
-  if (p.stream == kStreamSplit) return (int64_t)p.num_kv_heads * p.splits;
+  if (p.stream == kStreamSplit) return (int64_t)p.num_kv_heads * p.splits * split_qgroups(p);
   if (p.stream == kStreamRanges) return (int64_t)p.splits + (int64_t)p.num_segments * p.num_kv_heads;
   return attend_max_items(p);
 }

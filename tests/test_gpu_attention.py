@@ -40,9 +40,10 @@ class TestUnified:
         (1, 1, 1, 128, torch.bfloat16), (1, 32, 16, 256, torch.bfloat16), (1, 32, 8, 128, torch.bfloat16),
         (4, 4, 4, 64, torch.float32), (2, 8, 2, 256, torch.float32), (3, 6, 2, 128, torch.float16),
         (16, 2, 1, 64, torch.float32), (1, 1, 1, 512, torch.bfloat16), (1, 2, 1, 32, torch.float32),
-        # 5-8 query rows per kv head (split form reading keys and values)
+        # 5-16 query rows per kv head (split form reading keys and values, groups of 8 rows)
         (1, 64, 8, 128, torch.bfloat16), (1, 48, 8, 128, torch.bfloat16), (5, 1, 1, 128, torch.float16),
-        (2, 4, 1, 64, torch.bfloat16), (1, 16, 2, 256, torch.float32)])
+        (2, 4, 1, 64, torch.bfloat16), (1, 16, 2, 256, torch.float32), (1, 128, 8, 128, torch.bfloat16),
+        (1, 96, 8, 128, torch.bfloat16), (2, 8, 1, 64, torch.float16), (3, 4, 1, 128, torch.bfloat16)])
     def test_vs_oracle(self, dev, sq, hq, hkv, d, dtype):
         from orthocache_amd import _ops
 
