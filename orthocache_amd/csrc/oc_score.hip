@@ -47,6 +47,7 @@ __device__ __forceinline__ void load_rows(const char* tbase, int64_t stride64, u
 }
 
 constexpr int kMaxSegLds = 4096;  // segments whose offsets are staged in LDS
+constexpr int kWideBoundRows = 16;  // query rows per kv head of the single-reduction inline bound
 
 // Segment holding flattened block gb (binary search over cu staged in LDS).
 __device__ __forceinline__ int find_segment(const int* s_cu, int num_segments, int gb) {
@@ -413,7 +414,74 @@ void score_kernel(ScoreParams p) {
       best[k] = -INFINITY;
       sqrt_eac[k] = sqrtf(e_ac[k]);
     }
-    for (int q0 = 0; q0 < nq; q0 += 4) {
+    // (Variants with logits carry at most 4 rows, so only the others hold it.)
+    const bool wide = NQL == 0 && nq > 4 && nq <= kWideBoundRows;
+    if constexpr (NQL == 0) if (wide) {
+      // 5-16 query rows: every row's q.kbar and |q|^2 partials in one
+      // halving butterfly per wave (V - 1 exchanges for V values), one
+      // barrier, and the per-head maximum over the rows in wave 0, instead of
+      // a two-barrier workgroup sum per four rows.
+      constexpr int WQ = kWideBoundRows;
+      constexpr int V = 2 * WQ * HPT;  // value (k * WQ + u) * 2 + {0: q.kbar, 1: |q|^2}
+      static_assert(V <= kWave, "one value per lane after the butterfly");
+      float qv[WQ][NI];
+#pragma unroll
+      for (int u = 0; u < WQ; ++u) {
+        const int qi = min(u, nq - 1);
+        const int st = qi / p.group, g = qi - st * p.group;
+        const int64_t qoff = (int64_t)seg * p.q_seg_stride + (int64_t)st * p.q_tok_stride +
+                             (int64_t)(h0 * p.group + g) * p.q_head_stride;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) qv[u][i] = EQ::load1(p.q, qoff + qcol_off(min(t + 256 * i, DW - 1)));
+      }
+      float val[V];
+#pragma unroll
+      for (int k = 0; k < HPT; ++k)
+#pragma unroll
+        for (int u = 0; u < WQ; ++u) {
+          float a = 0.f, b = 0.f;
+#pragma unroll
+          for (int i = 0; i < NI; ++i) {
+            const int d = t + 256 * i;
+            const float v = (d < DW && (HPT == 1 || d / D == k)) ? qv[u][i] : 0.f;
+            a = fmaf(v, kbar_r[i], a);
+            b = fmaf(v, v, b);
+          }
+          val[(k * WQ + u) * 2] = a;
+          val[(k * WQ + u) * 2 + 1] = b;
+        }
+      const int lane = t & (kWave - 1), wave = t / kWave;
+      Butterfly<V, V, kWave / 2, kWave>::run(val, lane);
+      // Lane l now holds the wave's sum of value l / (64 / V).  The column
+      // merge is done with s_mean (block_sum's barriers came after it).
+      constexpr int REPV = kWave / V;
+      float* red = s_mean;
+      if (lane % REPV == 0) red[wave * V + lane / REPV] = val[0];
+      __syncthreads();
+      if (wave == 0) {
+        float bnd = -INFINITY;
+        if (lane < V && (lane & 1) == 0) {
+          float a = 0.f, b = 0.f;
+#pragma unroll
+          for (int w = 0; w < 256 / kWave; ++w) {
+            a += red[w * V + lane];
+            b += red[w * V + lane + 1];
+          }
+          const int k = (lane >> 1) / WQ, u = (lane >> 1) % WQ;
+          float se = sqrt_eac[0];
+#pragma unroll
+          for (int kk = 1; kk < HPT; ++kk) se = k == kk ? sqrt_eac[kk] : se;
+          if (u < nq) bnd = a / sqrt_d + (sqrtf(b) * se) / sqrt_d;
+        }
+        // The rows of head k sit at lanes 2 WQ k + 2 u: maximum over u
+        // (NaN-propagating) within each 2 WQ-lane window.
+#pragma unroll
+        for (int o = 2; o < 2 * WQ; o <<= 1) bnd = nanmax(bnd, __shfl_xor(bnd, o, kWave));
+#pragma unroll
+        for (int k = 0; k < HPT; ++k) best[k] = __shfl(bnd, 2 * WQ * k, kWave);
+      }
+    }
+    for (int q0 = 0; q0 < (wide ? 0 : nq); q0 += 4) {
       float qv[4][NI];
       if (prefetch && q0 == 0) {
 #pragma unroll
