@@ -47,6 +47,7 @@ __device__ __forceinline__ void load_rows(const char* tbase, int64_t stride64, u
 }
 
 constexpr int kMaxSegLds = 4096;  // segments whose offsets are staged in LDS
+template <int N> struct IntTag { static constexpr int value = N; };  // a row count as a type
 constexpr int kWideBoundRows = 16;  // query rows per kv head of the single-reduction inline bound
 
 // Segment holding flattened block gb (binary search over cu staged in LDS).
@@ -414,14 +415,15 @@ void score_kernel(ScoreParams p) {
       best[k] = -INFINITY;
       sqrt_eac[k] = sqrtf(e_ac[k]);
     }
-    // (Variants with logits carry at most 4 rows, so only the others hold it.)
-    const bool wide = NQL == 0 && nq > 4 && nq <= kWideBoundRows;
-    if constexpr (NQL == 0) if (wide) {
-      // 5-16 query rows: every row's q.kbar and |q|^2 partials in one
-      // halving butterfly per wave (V - 1 exchanges for V values), one
-      // barrier, and the per-head maximum over the rows in wave 0, instead of
-      // a two-barrier workgroup sum per four rows.
-      constexpr int WQ = kWideBoundRows;
+    // Up to WQ query rows at once: every row's q.kbar and |q|^2 partials in
+    // one halving butterfly per wave (V - 1 exchanges for V values), one
+    // barrier, and the per-head maximum over the rows in wave 0 (instead of a
+    // two-barrier workgroup sum per four rows: C2's scoring 88.5 -> 86.5 us,
+    // 16 rows per kv head 80.6 -> 45 us).  WQ = 4 for 1-4 rows, 16 for 5-16
+    // (variants without logits: those with logits carry at most 4 rows);
+    // more rows take the loop below.
+    auto bound_rows = [&](auto wq_tag) {
+      constexpr int WQ = decltype(wq_tag)::value;
       constexpr int V = 2 * WQ * HPT;  // value (k * WQ + u) * 2 + {0: q.kbar, 1: |q|^2}
       static_assert(V <= kWave, "one value per lane after the butterfly");
       float qv[WQ][NI];
@@ -432,7 +434,8 @@ void score_kernel(ScoreParams p) {
         const int64_t qoff = (int64_t)seg * p.q_seg_stride + (int64_t)st * p.q_tok_stride +
                              (int64_t)(h0 * p.group + g) * p.q_head_stride;
 #pragma unroll
-        for (int i = 0; i < NI; ++i) qv[u][i] = EQ::load1(p.q, qoff + qcol_off(min(t + 256 * i, DW - 1)));
+        for (int i = 0; i < NI; ++i)
+          qv[u][i] = (prefetch && u < 4) ? qpre[u][i] : EQ::load1(p.q, qoff + qcol_off(min(t + 256 * i, DW - 1)));
       }
       float val[V];
 #pragma unroll
@@ -480,6 +483,12 @@ void score_kernel(ScoreParams p) {
 #pragma unroll
         for (int k = 0; k < HPT; ++k) best[k] = __shfl(bnd, 2 * WQ * k, kWave);
       }
+    };
+    const bool wide = nq > 0 && nq <= kWideBoundRows && (NQL == 0 || nq <= 4);
+    if (nq > 0 && nq <= 4) {
+      bound_rows(IntTag<4>{});
+    } else if constexpr (NQL == 0) {
+      if (wide) bound_rows(IntTag<kWideBoundRows>{});
     }
     for (int q0 = 0; q0 < (wide ? 0 : nq); q0 += 4) {
       float qv[4][NI];
