@@ -48,6 +48,9 @@ __device__ __forceinline__ void load_rows(const char* tbase, int64_t stride64, u
 
 constexpr int kMaxSegLds = 4096;  // segments whose offsets are staged in LDS
 template <int N> struct IntTag { static constexpr int value = N; };  // a row count as a type
+template <bool B> struct BoolTag { static constexpr bool value = B; };
+constexpr int pow2_at_least(int n) { return n <= 1 ? 1 : 2 * pow2_at_least((n + 1) / 2); }
+constexpr int kScoreRed = 256;  // floats of the epilogue's reduction scratch
 constexpr int kWideBoundRows = 16;  // query rows per kv head of the single-reduction inline bound
 
 // Segment holding flattened block gb (binary search over cu staged in LDS).
@@ -98,7 +101,7 @@ void score_kernel(ScoreParams p) {
   constexpr int NI = (DW + 255) / 256;  // tile columns per thread in the epilogue
   __shared__ float s_mean[NSLOT * DW];
   __shared__ float s_m2[NSLOT * DW];
-  __shared__ float s_red[64];
+  __shared__ float s_red[kScoreRed];
   __shared__ int s_cu[kMaxSegLds + 1];
   __shared__ __attribute__((aligned(16))) float s_lg[NQL > 0 ? HPT * kBlock * NQL : 4];
 
@@ -382,15 +385,29 @@ void score_kernel(ScoreParams p) {
     tot[3 * k + 1] = (HPT == 1 || hh == k) ? mid : 0.f;
     tot[3 * k + 2] = elow[k];
   }
-  block_sum<3 * HPT>(tot, s_red);
-  float e_ac[HPT], zeta[HPT];
+  // The segment of this block (s_cu was filled before the key stream; the
+  // barrier after the statistics has made it visible).
+  if (NQL == 0 && need_seg) seg = find_segment(s_cu, p.num_segments, gb);
+
+  // Up to 16 query rows per kv head take the inline bound in one reduction
+  // (WQ = 4 for 1-4 rows, 16 for 5-16 in the variants without logits; those
+  // with logits carry at most 4 rows).  With one kv head per tile, or 1-4
+  // rows, the band totals ride in that same reduction (fused), so the tile
+  // has one reduction barrier in all; otherwise they take block_sum first.
+  const bool wide = want_bound && nq > 0 && nq <= kWideBoundRows && (NQL == 0 || nq <= 4);
+  const bool fused = want_bound && nq > 0 && (nq <= 4 || (wide && HPT == 1));
+  float e_ac[HPT], zeta[HPT], sqrt_eac[HPT], best[HPT];
 #pragma unroll
-  for (int k = 0; k < HPT; ++k) {
-    const float e_high = 0.5f * tot[3 * k];
-    const float e_mid = 0.125f * tot[3 * k + 1];
-    const float e_low = 0.125f * tot[3 * k + 2];
+  for (int k = 0; k < HPT; ++k) best[k] = -INFINITY;
+  // Energies, E_AC and zeta of head k from its three band totals; thread 0
+  // stores them.
+  auto finish_bands = [&](int k, float t_high, float t_mid, float t_low) {
+    const float e_high = 0.5f * t_high;
+    const float e_mid = 0.125f * t_mid;
+    const float e_low = 0.125f * t_low;
     e_ac[k] = e_low + e_mid + e_high;
     zeta[k] = e_high / (e_low + 1e-6f);  // spectral_energy.py:138
+    sqrt_eac[k] = sqrtf(e_ac[k]);
     if (t == 0) {
       if (p.e_low) p.e_low[tile0 + k] = e_low;
       if (p.e_mid) p.e_mid[tile0 + k] = e_mid;
@@ -398,34 +415,32 @@ void score_kernel(ScoreParams p) {
       if (p.e_ac) p.e_ac[tile0 + k] = e_ac[k];
       if (p.zeta) p.zeta[tile0 + k] = zeta[k];
     }
+  };
+  if (!fused) {
+    block_sum<3 * HPT>(tot, s_red);
+#pragma unroll
+    for (int k = 0; k < HPT; ++k) finish_bands(k, tot[3 * k], tot[3 * k + 1], tot[3 * k + 2]);
   }
 
   // Inline query-aware bound: tau_j = q.kbar/sqrt(d) + ||q|| sqrt(E_AC)/sqrt(d),
   // max over the segment's queries of every query head sharing kv head h.
-  if (NQL == 0 && need_seg) {
-    // s_cu was filled before the key stream; block_sum's barriers have
-    // made it visible.
-    seg = find_segment(s_cu, p.num_segments, gb);
-  }
   if (want_bound) {
     const float sqrt_d = sqrtf((float)D);
-    float best[HPT], sqrt_eac[HPT];
-#pragma unroll
-    for (int k = 0; k < HPT; ++k) {
-      best[k] = -INFINITY;
-      sqrt_eac[k] = sqrtf(e_ac[k]);
-    }
-    // Up to WQ query rows at once: every row's q.kbar and |q|^2 partials in
-    // one halving butterfly per wave (V - 1 exchanges for V values), one
-    // barrier, and the per-head maximum over the rows in wave 0 (instead of a
-    // two-barrier workgroup sum per four rows: C2's scoring 88.5 -> 86.5 us,
-    // 16 rows per kv head 80.6 -> 45 us).  WQ = 4 for 1-4 rows, 16 for 5-16
-    // (variants without logits: those with logits carry at most 4 rows);
-    // more rows take the loop below.
-    auto bound_rows = [&](auto wq_tag) {
+    // WQ query rows at once: every row's q.kbar and |q|^2 partials (and with
+    // FUSE the band totals) in one halving butterfly per wave (V - 1
+    // exchanges for V values), one barrier, and the per-head maximum over the
+    // rows in wave 0 (instead of a two-barrier workgroup sum per four rows:
+    // C2's scoring 88.5 -> 86.5 us, 16 rows per kv head 80.6 -> 45 us).  The
+    // per-wave sums pair lanes in the order wave_sum does and the waves are
+    // added in block_sum's order, so fused band totals are bit-identical to
+    // block_sum's.
+    auto bound_rows = [&](auto wq_tag, auto fuse_tag) {
       constexpr int WQ = decltype(wq_tag)::value;
-      constexpr int V = 2 * WQ * HPT;  // value (k * WQ + u) * 2 + {0: q.kbar, 1: |q|^2}
-      static_assert(V <= kWave, "one value per lane after the butterfly");
+      constexpr bool FUSE = decltype(fuse_tag)::value;
+      constexpr int NBV = 2 * WQ * HPT;  // value (k * WQ + u) * 2 + {0: q.kbar, 1: |q|^2}
+      constexpr int NV = FUSE ? NBV + 3 * HPT : NBV;  // then head k's band totals at NBV + 3 k
+      constexpr int V = pow2_at_least(NV);
+      static_assert(V <= kWave && V * (256 / kWave) <= kScoreRed, "one value per lane after the butterfly");
       float qv[WQ][NI];
 #pragma unroll
       for (int u = 0; u < WQ; ++u) {
@@ -453,22 +468,37 @@ void score_kernel(ScoreParams p) {
           val[(k * WQ + u) * 2] = a;
           val[(k * WQ + u) * 2 + 1] = b;
         }
+#pragma unroll
+      for (int i = NBV; i < V; ++i) val[i] = (FUSE && i < NV) ? tot[i - NBV] : 0.f;
       const int lane = t & (kWave - 1), wave = t / kWave;
       Butterfly<V, V, kWave / 2, kWave>::run(val, lane);
-      // Lane l now holds the wave's sum of value l / (64 / V).  The column
-      // merge is done with s_mean (block_sum's barriers came after it).
+      // Lane l now holds the wave's sum of value l / (64 / V).  (Unfused,
+      // block_sum's second barrier has released s_red.)
       constexpr int REPV = kWave / V;
-      float* red = s_mean;
-      if (lane % REPV == 0) red[wave * V + lane / REPV] = val[0];
+      if (lane % REPV == 0) s_red[wave * V + lane / REPV] = val[0];
       __syncthreads();
       if (wave == 0) {
+        if constexpr (FUSE) {
+#pragma unroll
+          for (int k = 0; k < HPT; ++k) {
+            float tt[3];
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+              float s = 0.f;
+#pragma unroll
+              for (int w = 0; w < 256 / kWave; ++w) s += s_red[w * V + NBV + 3 * k + j];
+              tt[j] = s;
+            }
+            finish_bands(k, tt[0], tt[1], tt[2]);
+          }
+        }
         float bnd = -INFINITY;
-        if (lane < V && (lane & 1) == 0) {
+        if (lane < NBV && (lane & 1) == 0) {
           float a = 0.f, b = 0.f;
 #pragma unroll
           for (int w = 0; w < 256 / kWave; ++w) {
-            a += red[w * V + lane];
-            b += red[w * V + lane + 1];
+            a += s_red[w * V + lane];
+            b += s_red[w * V + lane + 1];
           }
           const int k = (lane >> 1) / WQ, u = (lane >> 1) % WQ;
           float se = sqrt_eac[0];
@@ -484,11 +514,14 @@ void score_kernel(ScoreParams p) {
         for (int k = 0; k < HPT; ++k) best[k] = __shfl(bnd, 2 * WQ * k, kWave);
       }
     };
-    const bool wide = nq > 0 && nq <= kWideBoundRows && (NQL == 0 || nq <= 4);
-    if (nq > 0 && nq <= 4) {
-      bound_rows(IntTag<4>{});
-    } else if constexpr (NQL == 0) {
-      if (wide) bound_rows(IntTag<kWideBoundRows>{});
+    if (fused) {
+      if (nq <= 4) {
+        bound_rows(IntTag<4>{}, BoolTag<true>{});
+      } else if constexpr (NQL == 0 && HPT == 1) {
+        bound_rows(IntTag<kWideBoundRows>{}, BoolTag<true>{});
+      }
+    } else if (wide) {
+      if constexpr (NQL == 0) bound_rows(IntTag<kWideBoundRows>{}, BoolTag<false>{});
     }
     for (int q0 = 0; q0 < (wide ? 0 : nq); q0 += 4) {
       float qv[4][NI];
