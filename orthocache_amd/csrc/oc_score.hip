@@ -721,6 +721,160 @@ __global__ __launch_bounds__(256) void bound_kernel(BoundParams p) {
   }
 }
 
+// Exact three-term bf16 split of an fp32 value: x = hi + mid + lo, each term
+// a bf16 value (returned as fp32 bit patterns whose low 16 bits are zero).
+// hi keeps the top 8 of x's 24 significant bits, mid the top 8 of the
+// remainder, and lo the rest (at most 8 bits), so the sum is exact for every
+// finite x above the subnormal range; +-inf gives (inf, 0, 0) and NaN a NaN hi.
+__device__ __forceinline__ void split_bf16x3(float x, uint32_t& hb, uint32_t& mb, uint32_t& lb) {
+  hb = (x != x) ? 0x7FC00000u : (__float_as_uint(x) & 0xFFFF0000u);
+  const float r1 = __builtin_isinf(x) ? 0.f : x - __uint_as_float(hb);
+  mb = __float_as_uint(r1) & 0xFFFF0000u;
+  const float r2 = r1 - __uint_as_float(mb);
+  lb = __float_as_uint(r2) & 0xFFFF0000u;
+}
+
+// bound_kernel for bf16 queries on the bf16 matrix cores.  q is exact in bf16
+// and kbar = dc / sqrt(512) (fp32) is split exactly into three bf16 terms, so
+// q.kbar is the sum of three bf16 products, each exact, accumulated in fp32
+// by v_mfma_f32_32x32x16_bf16 -- the fp32 kernel's arithmetic, at three
+// 8-pass products per 16 dims instead of eight 16-pass fp32 ones.  A
+// workgroup covers NQT query tiles of 64 rows against 64 blocks of one kv
+// head; each wave splits its 32 blocks' kbar chunk once per 16 dims and uses
+// it for all NQT tiles.  MFMA lane l supplies row l % 32 and k indices
+// 8 (l / 32) .. + 8, which map to dims hf * D/2 + s .. + 8 of both operands
+// (the contraction order is free as long as A and B agree).  |q|^2 comes
+// from packed dot products of the same query words.  Output lane l, i:
+// query 8(i/4) + 4(l/32) + i%4, block l % 32, as in bound_kernel.
+template <int NQT, int HALF>
+__global__ __launch_bounds__(256) void bound_bf16_kernel(BoundParams p) {
+  typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  __shared__ float s_m[NQT][2][2][32];
+  constexpr int D = 2 * HALF;
+  const int H = p.num_kv_heads;
+  const int nb = p.num_blocks;
+  const int nq = p.sq * p.group;
+  const int nbt = (nb + kBoundBT - 1) / kBoundBT;
+  int id = blockIdx.x;
+  const int h = id % H; id /= H;
+  const int bt = id % nbt;
+  const int qb = id / nbt;  // query tiles qb * NQT .. + NQT
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int wave = t / kWave;
+  const int wq = wave & 1, wb = wave >> 1;
+  const int r = lane & 31, hf = lane >> 5;
+
+  const int brow = bt * kBoundBT + wb * 32 + r;
+  const float* dcrow = p.dc + ((int64_t)min(brow, nb - 1) * H + h) * D;
+  const float eac = p.e_ac[(int64_t)min(brow, nb - 1) * H + h];
+  const int d0 = hf * HALF;
+  const uint16_t* qrow[NQT];
+#pragma unroll
+  for (int k = 0; k < NQT; ++k) {
+    const int qc = min((qb * NQT + k) * kBoundQT + wq * 32 + r, nq - 1);
+    const int st = qc / p.group, gq = qc - st * p.group;
+    qrow[k] = reinterpret_cast<const uint16_t*>(p.q) + (int64_t)st * p.q_tok_stride +
+              (int64_t)(h * p.group + gq) * p.q_head_stride + d0;
+  }
+  constexpr float kInv = 1.f / kSqrt512;
+  f32x16 acc[NQT];
+  float qq[NQT];
+#pragma unroll
+  for (int k = 0; k < NQT; ++k) {
+    qq[k] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[k][i] = 0.f;
+  }
+  // Rounds of 64 dims of the lane's half: all of a round's loads are issued
+  // before its products, so a wave waits for memory once per round.
+  constexpr int kSteps = HALF / 8 < 8 ? HALF / 8 : 8;  // 8 dims per product step
+#pragma unroll
+  for (int s0 = 0; s0 < HALF; s0 += 8 * kSteps) {
+    uint4 qa[kSteps][NQT];
+    float4 c[kSteps][2];
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) {
+      const int s = s0 + 8 * j;
+#pragma unroll
+      for (int k = 0; k < NQT; ++k) qa[j][k] = ld16(qrow[k] + s);
+      c[j][0] = *reinterpret_cast<const float4*>(dcrow + d0 + s);
+      c[j][1] = *reinterpret_cast<const float4*>(dcrow + d0 + s + 4);
+    }
+    // Keep the compiler from sinking the loads to their uses (it would wait
+    // for memory once per step).
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) {
+      const float kb[8] = {c[j][0].x * kInv, c[j][0].y * kInv, c[j][0].z * kInv, c[j][0].w * kInv,  // kbar, spectral_energy.py:166
+                           c[j][1].x * kInv, c[j][1].y * kInv, c[j][1].z * kInv, c[j][1].w * kInv};
+      uint4 bh, bm, bl;
+      uint32_t* ph = &bh.x;
+      uint32_t* pm = &bm.x;
+      uint32_t* pl = &bl.x;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t h0, m0, l0, h1, m1, l1;
+        split_bf16x3(kb[2 * i], h0, m0, l0);
+        split_bf16x3(kb[2 * i + 1], h1, m1, l1);
+        ph[i] = (h0 >> 16) | h1;
+        pm[i] = (m0 >> 16) | m1;
+        pl[i] = (l0 >> 16) | l1;
+      }
+      const bf16x8 vh = __builtin_bit_cast(bf16x8, bh);
+      const bf16x8 vm = __builtin_bit_cast(bf16x8, bm);
+      const bf16x8 vl = __builtin_bit_cast(bf16x8, bl);
+#pragma unroll
+      for (int k = 0; k < NQT; ++k) {
+        const bf16x8 va = __builtin_bit_cast(bf16x8, qa[j][k]);
+        acc[k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, vh, acc[k], 0, 0, 0);
+        acc[k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, vm, acc[k], 0, 0, 0);
+        acc[k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, vl, acc[k], 0, 0, 0);
+        qq[k] = dot2_acc<kBF16>(qa[j][k].x, qa[j][k].x, qq[k]);
+        qq[k] = dot2_acc<kBF16>(qa[j][k].y, qa[j][k].y, qq[k]);
+        qq[k] = dot2_acc<kBF16>(qa[j][k].z, qa[j][k].z, qq[k]);
+        qq[k] = dot2_acc<kBF16>(qa[j][k].w, qa[j][k].w, qq[k]);
+      }
+    }
+  }
+
+  // tau_j(q) = q.kbar/sqrt(d) + ||q|| sqrt(E_AC)/sqrt(d) (spectral_energy.py:170-176).
+  const float inv_sqrt_d = 1.f / sqrtf((float)D);
+  const float sqrt_eac = sqrtf(eac);
+#pragma unroll
+  for (int k = 0; k < NQT; ++k) {
+    const float qf = qq[k] + __shfl_xor(qq[k], 32, kWave);  // full squared norm of query row r
+    const int q0 = (qb * NQT + k) * kBoundQT + wq * 32;
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int rr = 8 * (i >> 2) + 4 * hf + (i & 3);
+      const float qn = __shfl(qf, rr, kWave);
+      if (q0 + rr < nq && brow < nb) {
+        const float bound = acc[k][i] * inv_sqrt_d + (sqrtf(qn) * sqrt_eac) * inv_sqrt_d;
+        if (p.bounds) p.bounds[((int64_t)(q0 + rr) * nb + brow) * H + h] = bound;
+        m = nanmax(m, bound);
+      }
+    }
+    if (p.tau_part) {
+      m = nanmax(m, __shfl_xor(m, 32, kWave));
+      if (hf == 0) s_m[k][wb][wq][r] = m;
+    }
+  }
+  if (p.tau_part) {
+    // NaN-propagating max over each tile's 64 queries: the two query-half
+    // waves through LDS.
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < NQT; ++k) {
+      const int qt = qb * NQT + k;
+      if (wq == 0 && hf == 0 && brow < nb && qt * kBoundQT < nq)
+        p.tau_part[((int64_t)qt * nb + brow) * H + h] = nanmax(s_m[k][wb][0][r], s_m[k][wb][1][r]);
+    }
+  }
+}
+
 // Query-aware bound from write-time block statistics: with kbar, E_AC and
 // zeta computed once when a block enters the cache (oc_score_blocks without
 // queries), a decode step only needs tau_j(q) = q.kbar/sqrt(d) +
@@ -927,6 +1081,21 @@ hipError_t launch_bound(const BoundParams& p, hipStream_t s) {
   const bool vec = (reinterpret_cast<uintptr_t>(p.q) % 16 == 0) && (reinterpret_cast<uintptr_t>(p.dc) % 16 == 0) &&
                    (p.q_tok_stride * qsz) % 16 == 0 && (p.q_head_stride * qsz) % 16 == 0 &&
                    p.head_dim % 2 == 0 && (half * qsz) % 16 == 0 && (half * 4) % 16 == 0;
+  if (p.q_dtype == kBF16 && vec) {
+    // bf16 queries, head_dim 64 / 128 / 256: the bf16 matrix cores with kbar
+    // split into three bf16 terms, one query tile per workgroup (C4, 2048
+    // rows x 256 blocks x 8 kv heads: 7.8 us against 8.5 us for the fp32
+    // kernel; two or four tiles per workgroup, sharing each split: 11.1 and
+    // 17.6 us).
+    constexpr int kNqt = 1;
+    const dim3 g2(((nqt + kNqt - 1) / kNqt) * nbt * p.num_kv_heads);
+    switch (p.head_dim) {
+      case 64: hipLaunchKernelGGL((bound_bf16_kernel<kNqt, 32>), g2, dim3(256), 0, s, p); return hipGetLastError();
+      case 128: hipLaunchKernelGGL((bound_bf16_kernel<kNqt, 64>), g2, dim3(256), 0, s, p); return hipGetLastError();
+      case 256: hipLaunchKernelGGL((bound_bf16_kernel<kNqt, 128>), g2, dim3(256), 0, s, p); return hipGetLastError();
+      default: break;  // other head dims: the fp32 kernel
+    }
+  }
   switch (p.q_dtype) {
     case kF32: launch_bound_q<kF32>(p, grid, vec, s); break;
     case kBF16: launch_bound_q<kBF16>(p, grid, vec, s); break;

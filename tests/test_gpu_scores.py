@@ -196,6 +196,53 @@ class TestBounds:
         ref = O.query_aware_bounds(O.fold_gqa(q, hkv), keys)
         np.testing.assert_allclose(b, ref, rtol=1e-5, atol=1e-5)
 
+    @pytest.mark.parametrize("sq,hq,hkv,d,nblk", [(100, 4, 2, 128, 70), (37, 8, 1, 64, 3), (65, 2, 2, 256, 5),
+                                                    (512, 4, 1, 128, 130), (17, 4, 4, 128, 1)])
+    def test_bf16_queries_many_rows(self, dev, sq, hq, hkv, d, nblk):
+        """Many bf16 query rows take the bf16 matrix-core bound (kbar split
+        into three bf16 terms): full bounds and per-64-row tile maxima against
+        the float64 oracle, and against the fp32 kernel on the same values.
+        Ragged query tiles (odd tile counts leave a workgroup's second tile
+        empty) and block counts that are not multiples of 64."""
+        import orthocache_amd as oc
+        from orthocache_amd import _ops
+
+        rng = np.random.default_rng(sq * 31 + nblk)
+        qd = to_dev(rng.standard_normal((sq, hq, d)).astype(np.float32), dev, torch.bfloat16)
+        kd = to_dev((rng.standard_normal((nblk * 512, hkv, d)) + 0.25).astype(np.float32), dev, torch.bfloat16)
+        q, keys = np32(qd), np32(kd)  # the values the GPU sees
+        ref = O.query_aware_bounds(O.fold_gqa(q, hkv), keys)
+        b = np32(oc.compute_query_aware_bounds(qd, kd))
+        np.testing.assert_allclose(b, ref, rtol=1e-5, atol=1e-5)
+        b32 = np32(oc.compute_query_aware_bounds(qd.float(), kd))
+        np.testing.assert_allclose(b, b32, rtol=2e-6, atol=2e-6)
+        parts = np32(_ops.score(kd, qd).tau_max)
+        nq = ref.shape[0]
+        nt = (nq + 63) // 64
+        pad = np.full((nt * 64 - nq,) + ref.shape[1:], -np.inf)
+        ref_parts = np.concatenate([ref, pad]).reshape(nt, 64, *ref.shape[1:]).max(axis=1)
+        assert parts.shape == ref_parts.shape
+        np.testing.assert_allclose(parts, ref_parts, rtol=1e-5, atol=1e-5)
+
+    def test_bf16_queries_nonfinite_keys(self, dev):
+        """Infinite and NaN keys: the bf16 split kernel's bounds equal the
+        fp32 kernel's (NaN where it gives NaN, the same infinities)."""
+        import orthocache_amd as oc
+
+        rng = np.random.default_rng(11)
+        k = rng.standard_normal((6 * 512, 2, 128)).astype(np.float32)
+        k[3, 0, 5] = np.inf
+        k[512 + 7, 1, 100] = -np.inf
+        k[2 * 512, 0, 0] = np.nan
+        k[4 * 512 + 1, 1, 64:] = 3e38
+        qd = to_dev(rng.standard_normal((70, 4, 128)).astype(np.float32), dev, torch.bfloat16)
+        kd = to_dev(k, dev, torch.bfloat16)
+        b = np32(oc.compute_query_aware_bounds(qd, kd))
+        b32 = np32(oc.compute_query_aware_bounds(qd.float(), kd))
+        assert np.array_equal(np.isnan(b), np.isnan(b32))
+        assert np.array_equal(np.isinf(b), np.isinf(b32))
+        np.testing.assert_allclose(b, b32, rtol=2e-6, atol=2e-6)
+
     @pytest.mark.parametrize("sq,hq,hkv", [(1, 32, 16), (2, 8, 2), (64, 4, 4), (1, 32, 8), (3, 9, 3)])
     @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
     def test_tau_max_inline_and_tiled(self, dev, sq, hq, hkv, dtype):
