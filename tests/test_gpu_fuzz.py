@@ -9,8 +9,9 @@ the oracle's bit for bit: mask_from_scores over the NaN-propagating maximum of
 the partial maxima (spectral_energy.py:180-234: jnp.max, then fp32 compares),
 then stream_compact_indices (compaction.py:65-82).  One segment with 1-3
 partial maxima per score, and ragged segments with per-segment thresholds;
-and given masks with the per-head lists.  Deterministic (derandomize), no
-example database.
+and given masks with the per-head lists.  Also the many-query bound of bf16
+queries over random shapes.  Deterministic (derandomize), no example
+database.
 """
 
 import numpy as np
@@ -133,3 +134,38 @@ def test_fuzz_given_mask_head_lists(m):
         oh, nh = O.stream_compact_indices(m[:, k])
         np.testing.assert_array_equal(hi[k], oh)
         assert int(hn[0, k]) == nh
+
+
+@st.composite
+def bound_shapes(draw):
+    d = draw(st.sampled_from([64, 128, 256]))
+    hkv = draw(st.sampled_from([1, 2, 4]))
+    group = draw(st.sampled_from([1, 2, 3, 4, 8]))
+    sq = draw(st.integers(1, 96))
+    nblk = draw(st.integers(1, 40))
+    shift = draw(st.sampled_from([0.0, 0.5, -2.0]))
+    seed = draw(st.integers(0, 2**31 - 1))
+    return d, hkv, group, sq, nblk, shift, seed
+
+
+@given(bound_shapes())
+@settings(derandomize=True, database=None, max_examples=20, deadline=None,
+          suppress_health_check=[HealthCheck.too_slow, HealthCheck.data_too_large])
+def test_fuzz_bf16_query_bounds(shape):
+    """Many-query bounds of bf16 queries (the bf16 matrix-core kernel, k̄
+    split into three bf16 terms) over random head dims, GQA groups, query
+    counts and block counts: against the float64 oracle
+    (spectral_energy.py:141-177) and against the fp32-MFMA kernel on the
+    same values."""
+    import orthocache_amd as oc
+
+    d, hkv, group, sq, nblk, shift, seed = shape
+    rng = np.random.default_rng(seed)
+    dev = _dev()
+    qd = torch.from_numpy(rng.standard_normal((sq, hkv * group, d)).astype(F32)).to(dev).to(torch.bfloat16)
+    kd = torch.from_numpy((rng.standard_normal((nblk * 512, hkv, d)) + shift).astype(F32)).to(dev).to(torch.bfloat16)
+    b = oc.compute_query_aware_bounds(qd, kd).float().cpu().numpy()
+    b32 = oc.compute_query_aware_bounds(qd.float(), kd).float().cpu().numpy()
+    np.testing.assert_allclose(b, b32, rtol=2e-6, atol=2e-6)
+    q, keys = qd.float().cpu().numpy(), kd.float().cpu().numpy()
+    np.testing.assert_allclose(b, O.query_aware_bounds(O.fold_gqa(q, hkv), keys), rtol=1e-5, atol=1e-5)
