@@ -67,8 +67,7 @@ __device__ __forceinline__ int find_segment(const int* s_cu, int num_segments, i
 // workgroups per CU without spilling (168 VGPRs): packed dot products
 // (16-bit keys and queries) with 32 lanes per row and two query rows, or bf16
 // with 16 lanes per row and four query rows.  Measured: the C2 shape (bf16,
-// head_dim 256) 90 us at three workgroups per CU against 97 us at two (its bf16
-// build now fits four); the C3 layer (head_dim 128, four query rows per kv
+// head_dim 256) 90 us at three workgroups per CU against 97 us at two; the C3 layer (head_dim 128, four query rows per kv
 // head) 363 us against 377 us.
 // The other bf16 logits variants are held to at least two.  (Some fp16
 // logits variants need more than 256 VGPRs as scheduled and would spill under
@@ -128,6 +127,17 @@ void score_kernel(ScoreParams p) {
   const uint32_t col_off =
       HPT == 1 ? (uint32_t)(cc * VEC * ESZ) : (uint32_t)(((int64_t)hh * p.k_head_stride + cw) * ESZ);
   auto lane_off = [&](int l) -> uint32_t { return (uint32_t)(l * (uint32_t)row_bytes) + col_off; };
+  // 16-bit variants with logits and one kv head per tile request their first
+  // eight rows before anything else (query prefetch, segment table, address
+  // set-up), so every workgroup's key stream starts as early as it can.  C2's
+  // variant then takes 130 VGPRs and three workgroups per CU instead of 124
+  // and four, and is still faster: scoring 86.4 -> 85.4 us (forcing four
+  // workgroups spills: 88.3 us).  The other variants keep the later request:
+  // several of them would lose a workgroup per CU, and neither C3's (two heads
+  // per tile: 197.1 -> 197.7 us) nor C5's (823.3 -> 824.2 us) gained.
+  constexpr bool kEarlyRows = NQL > 0 && DT != kF32 && HPT == 1;
+  uint4 ra[8], rb[8];
+  if constexpr (kEarlyRows) load_rows(tbase, stride64, lane_off(slot), ra);
   // Query element offset of tile column dcol (head h0 + dcol / D, dim dcol % D).
   auto qcol_off = [&](int dcol) -> int64_t {
     if constexpr (HPT == 1) return dcol;
@@ -252,7 +262,7 @@ void score_kernel(ScoreParams p) {
       // bf16: the partial sums are reduced and staged before the statistics,
       // which then widen one column at a time, so the sums and the widened
       // rows are never live together.  C2's variant (head_dim 256, two query
-      // rows) needs 125 VGPRs, four workgroups per CU, against 136 and three
+      // rows) needed 125 VGPRs, four workgroups per CU, against 136 and three
       // (scoring 90.8 -> 89.2 us); four query rows 162 against 172-198.
       reduce_store(part, l);
 #pragma unroll
@@ -279,8 +289,7 @@ void score_kernel(ScoreParams p) {
     if constexpr (NQL > 0) reduce_store(part, l);
   };
 
-  uint4 ra[8], rb[8];
-  load_rows(tbase, stride64, lane_off(slot), ra);
+  if constexpr (!kEarlyRows) load_rows(tbase, stride64, lane_off(slot), ra);
   int seg = 0;
   if constexpr (NQL > 0) {
     // The logits need this block's queries before the first rows arrive: in
